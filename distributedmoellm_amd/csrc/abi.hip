@@ -1,0 +1,233 @@
+// Exported C entry points (declared in include/moehip.h): argument checks,
+// then the kernels of matvec.hip / dequant.hip / layer.hip.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/moehip.h"
+#include "common.h"
+#include "dequant.h"
+#include "layer.h"
+#include "matvec.h"
+
+static_assert(sizeof(moe_q4_expert) == sizeof(moe::ExpertDesc), "moe_q4_expert layout");
+static_assert(offsetof(moe_q4_expert, xor8) == offsetof(moe::ExpertDesc, xor8), "moe_q4_expert layout");
+
+namespace moe {
+
+static thread_local char g_err[1024];
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MOE_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return MOE_OK;
+}
+
+static hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define REQUIRE(cond, ...)                      \
+  do {                                          \
+    if (!(cond)) return set_error(MOE_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+static int check_group_shape(const char* who, int O, int I, int gs) {
+  REQUIRE(O > 0 && I > 0, "%s: O=%d and I=%d must be positive", who, O, I);
+  REQUIRE(gs > 0 && I % gs == 0, "%s: group size %d must divide I=%d", who, gs, I);
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+MOE_API int moe_version(void) { return 100; }
+
+MOE_API const char* moe_last_error(void) { return g_err; }
+
+MOE_API int moe_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+MOE_API int moe_device_info(int device, char* buf, int len) {
+  REQUIRE(buf != nullptr && len > 0, "moe_device_info: no buffer");
+  hipDeviceProp_t p;
+  const hipError_t e = hipGetDeviceProperties(&p, device);
+  if (e != hipSuccess) return set_error(MOE_EHIP, "moe_device_info(%d): %s", device, hipGetErrorString(e));
+  snprintf(buf, (size_t)len, "%s|%s|%d|%d|%zu", p.name, p.gcnArchName, p.multiProcessorCount, p.clockRate,
+           (size_t)p.totalGlobalMem);
+  return MOE_OK;
+}
+
+MOE_API int moe_init(int device) {
+  const int n = moe_device_count();
+  REQUIRE(n > 0, "moe_init: no HIP device is visible");
+  REQUIRE(device >= 0 && device < n, "moe_init: device %d of %d", device, n);
+  hipDeviceProp_t p;
+  const hipError_t e = hipGetDeviceProperties(&p, device);
+  if (e != hipSuccess) return set_error(MOE_EHIP, "moe_init(%d): %s", device, hipGetErrorString(e));
+  REQUIRE(strncmp(p.gcnArchName, "gfx950", 6) == 0, "moe_init: device %d is %s; these kernels are built for gfx950",
+          device, p.gcnArchName);
+  return MOE_OK;
+}
+
+// ------------------------------------------------------------------ mat-vec
+
+MOE_API int moe_q4_matmul_t(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I,
+                            int gs, int offset, float* y, void* stream) {
+  if (int rc = check_group_shape("moe_q4_matmul_t", O, I, gs)) return rc;
+  REQUIRE(I % 2 == 0 && gs % 2 == 0, "moe_q4_matmul_t: I=%d and gs=%d must be even", I, gs);
+  REQUIRE(n >= 0, "moe_q4_matmul_t: n=%d", n);
+  if (n == 0) return MOE_OK;
+  REQUIRE(x && raw && s && y, "moe_q4_matmul_t: null pointer");
+  MVShape sh;
+  plan_matvec(FMT_Q4, O, I, gs, &sh);
+  MVJob j{};
+  j.x = x;
+  j.ldx = I;
+  j.y = y;
+  j.ldy = O;
+  j.n = n;
+  j.single = MatRef{raw, s, offset ? 0u : 0x88888888u, s_f16};
+  return run_matvec(FMT_Q4, sh, j, 1, n, as_stream(stream));
+}
+
+MOE_API int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* s, int s_f16, int O, int I, int gs,
+                            float* y, void* stream) {
+  if (int rc = check_group_shape("moe_q8_matmul_t", O, I, gs)) return rc;
+  REQUIRE(n >= 0, "moe_q8_matmul_t: n=%d", n);
+  if (n == 0) return MOE_OK;
+  REQUIRE(x && q && s && y, "moe_q8_matmul_t: null pointer");
+  MVShape sh;
+  plan_matvec(FMT_Q8, O, I, gs, &sh);
+  MVJob j{};
+  j.x = x;
+  j.ldx = I;
+  j.y = y;
+  j.ldy = O;
+  j.n = n;
+  j.single = MatRef{reinterpret_cast<const uint8_t*>(q), s, 0u, s_f16};
+  return run_matvec(FMT_Q8, sh, j, 1, n, as_stream(stream));
+}
+
+MOE_API int moe_gguf_matmul_t(const float* x, int n, const uint8_t* raw, int qtype, int O, int cols, float* y,
+                              void* stream) {
+  REQUIRE(qtype == FMT_Q8_0 || qtype == FMT_Q4_K, "moe_gguf_matmul_t: qtype %d (supported: 8 Q8_0, 12 Q4_K)",
+          qtype);
+  const int blk = qtype == FMT_Q8_0 ? 32 : 256;
+  REQUIRE(O > 0 && cols > 0 && cols % blk == 0, "moe_gguf_matmul_t: cols=%d must be a positive multiple of %d",
+          cols, blk);
+  REQUIRE(n >= 0, "moe_gguf_matmul_t: n=%d", n);
+  if (n == 0) return MOE_OK;
+  REQUIRE(x && raw && y, "moe_gguf_matmul_t: null pointer");
+  MVShape sh;
+  plan_matvec(qtype, O, cols, blk, &sh);
+  MVJob j{};
+  j.x = x;
+  j.ldx = cols;
+  j.y = y;
+  j.ldy = O;
+  j.n = n;
+  j.single = MatRef{raw, nullptr, 0u, 0};
+  return run_matvec(qtype, sh, j, 1, n, as_stream(stream));
+}
+
+// ------------------------------------------------------------------ dequant
+
+MOE_API int moe_q4_dequant(const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs, int offset,
+                           float* out, void* stream) {
+  if (int rc = check_group_shape("moe_q4_dequant", O, I, gs)) return rc;
+  REQUIRE(I % 2 == 0, "moe_q4_dequant: I=%d must be even", I);
+  REQUIRE(raw && s && out, "moe_q4_dequant: null pointer");
+  return run_dequant_q4(raw, s, s_f16, O, I, gs, offset ? 0u : 0x88u, out, as_stream(stream));
+}
+
+MOE_API int moe_q8_dequant(const int8_t* q, const void* s, int s_f16, int O, int I, int gs, float* out,
+                           void* stream) {
+  if (int rc = check_group_shape("moe_q8_dequant", O, I, gs)) return rc;
+  REQUIRE(q && s && out, "moe_q8_dequant: null pointer");
+  return run_dequant_q8(q, s, s_f16, O, I, gs, out, as_stream(stream));
+}
+
+MOE_API int moe_gguf_dequant(const uint8_t* raw, int qtype, int O, int cols, float* out, void* stream) {
+  REQUIRE(qtype == FMT_Q8_0 || qtype == FMT_Q4_K, "moe_gguf_dequant: qtype %d (supported: 8 Q8_0, 12 Q4_K)", qtype);
+  const int blk = qtype == FMT_Q8_0 ? 32 : 256;
+  REQUIRE(O > 0 && cols > 0 && cols % blk == 0, "moe_gguf_dequant: cols=%d must be a positive multiple of %d", cols,
+          blk);
+  REQUIRE(raw && out, "moe_gguf_dequant: null pointer");
+  return run_dequant_gguf(raw, qtype, O, cols, out, as_stream(stream));
+}
+
+// ------------------------------------------------------------------ fused layer
+
+MOE_API size_t moe_q4_layer_workspace(int P, int H, int I) {
+  if (P <= 0 || H <= 0 || I <= 0) return 0;
+  return q4_layer_workspace(P, H, I);
+}
+
+MOE_API int moe_q4_layer(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k,
+                         const int* poff, const int* prow, const float* pw, int P, const int* rrow, const int* rptr,
+                         const int* rpair, int nr, float* out, int ldo, int H, int I, int gs, int max_rows,
+                         void* workspace, size_t ws_bytes, void* stream) {
+  REQUIRE(H > 0 && I > 0 && H % 2 == 0 && I % 2 == 0, "moe_q4_layer: H=%d and I=%d must be positive and even", H, I);
+  REQUIRE(gs > 0 && gs % 2 == 0 && H % gs == 0 && I % gs == 0, "moe_q4_layer: group size %d must divide H=%d and I=%d",
+          gs, H, I);
+  REQUIRE(k >= 0 && P >= 0 && nr >= 0, "moe_q4_layer: k=%d P=%d nr=%d", k, P, nr);
+  if (k == 0 || P == 0) return MOE_OK;
+  REQUIRE(max_rows > 0 && max_rows <= P, "moe_q4_layer: max_rows=%d for P=%d", max_rows, P);
+  REQUIRE(ldx >= H && ldo >= H, "moe_q4_layer: ldx=%d ldo=%d must be >= H=%d", ldx, ldo, H);
+  REQUIRE(x && table && poff && prow && pw && rrow && rptr && rpair && out, "moe_q4_layer: null pointer");
+  const size_t need = q4_layer_workspace(P, H, I);
+  if (workspace == nullptr || ws_bytes < need)
+    return set_error(MOE_EWORKSPACE, "moe_q4_layer: workspace of %zu bytes, %zu needed", ws_bytes, need);
+  REQUIRE(aligned(workspace, 16), "moe_q4_layer: workspace must be 16-byte aligned");
+  Q4LayerArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.table = reinterpret_cast<const ExpertDesc*>(table);
+  a.eidx = eidx;
+  a.k = k;
+  a.poff = poff;
+  a.prow = prow;
+  a.pw = pw;
+  a.P = P;
+  a.rrow = rrow;
+  a.rptr = rptr;
+  a.rpair = rpair;
+  a.nr = nr;
+  a.out = out;
+  a.ldo = ldo;
+  a.H = H;
+  a.I = I;
+  a.gs = gs;
+  a.max_rows = max_rows;
+  a.workspace = workspace;
+  return run_q4_layer(a, as_stream(stream));
+}
+
+MOE_API int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, void* stream) {
+  REQUIRE(n >= 0 && I > 0 && ldh >= 2 * I && lda >= I, "moe_silu_mul: n=%d I=%d ldh=%d lda=%d", n, I, ldh, lda);
+  if (n == 0) return MOE_OK;
+  REQUIRE(h && a, "moe_silu_mul: null pointer");
+  return run_silu_mul(h, ldh, n, I, a, lda, as_stream(stream));
+}
+
+MOE_API int moe_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair,
+                        int nr, float* out, int ldo, int H, void* stream) {
+  REQUIRE(nr >= 0 && H > 0 && ldy >= H && ldo >= H, "moe_combine: nr=%d H=%d ldy=%d ldo=%d", nr, H, ldy, ldo);
+  if (nr == 0) return MOE_OK;
+  REQUIRE(y && pw && rrow && rptr && rpair && out, "moe_combine: null pointer");
+  return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, as_stream(stream));
+}

@@ -1,0 +1,74 @@
+// Shared helpers for the routed-expert HIP kernels (gfx950, wave64).
+//
+// Every exported entry point validates its arguments on the host, records a
+// readable message with set_error() on failure and returns a non-zero status;
+// moe_last_error() hands the message to the caller (thread-local, like errno).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#define MOE_API extern "C" __attribute__((visibility("default")))
+
+// status codes shared with include/moehip.h
+#define MOE_OK 0
+#define MOE_EINVAL 1      // bad argument (shape, pointer, size)
+#define MOE_EHIP 2        // a HIP runtime call failed
+#define MOE_EWORKSPACE 3  // caller's workspace too small
+#define MOE_EUNSUPPORTED 4
+
+namespace moe {
+
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// hipGetLastError() after a launch; returns MOE_OK or MOE_EHIP with the message set
+int check_launch(const char* what);
+
+__host__ __device__ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes that are read once: a non-temporal 128-bit load
+__device__ __forceinline__ uint4 stream_load16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
+// ---------------------------------------------------------------- device helpers
+
+// An empty asm that hides a value's known bits from the optimiser, so
+// (v >> 8k) & 0xFF on a nibble-masked word maps to one v_cvt_f32_ubyteK.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ float ubyte(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+  return __half2float(__ushort_as_half((unsigned short)h));
+}
+
+// Group scales are f16 or f32, chosen per call.
+__device__ __forceinline__ float load_scale(const void* s, size_t idx, int f16) {
+  return f16 ? half_bits_to_float(reinterpret_cast<const uint16_t*>(s)[idx])
+             : reinterpret_cast<const float*>(s)[idx];
+}
+
+// GGUF f16 fields: llama.cpp-style decode, except that exponent 31 (Inf and NaN)
+// reads as a signed infinity (moelan/kernels.py:244-255).
+__device__ __forceinline__ float gguf_half(uint32_t h) {
+  if ((h & 0x7C00u) == 0x7C00u) return (h & 0x8000u) ? -INFINITY : INFINITY;
+  return half_bits_to_float(h);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// sum over aligned groups of `width` lanes (width a power of two <= 64)
+__device__ __forceinline__ float group_sum(float v, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace moe

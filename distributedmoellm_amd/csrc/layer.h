@@ -1,0 +1,33 @@
+#pragma once
+#include "common.h"
+#include "matvec.h"
+
+namespace moe {
+
+struct Q4LayerArgs {
+  const float* x;
+  int ldx;
+  const ExpertDesc* table;
+  const int* eidx;
+  int k;
+  const int* poff;   // [k+1]
+  const int* prow;   // [P] input row of each pair
+  const float* pw;   // [P] gate weight of each pair
+  int P;
+  const int* rrow;   // [nr] touched rows, each once
+  const int* rptr;   // [nr+1]
+  const int* rpair;  // [P] pairs of each touched row, ascending
+  int nr;
+  float* out;
+  int ldo;
+  int H, I, gs, max_rows;
+  void* workspace;
+};
+
+size_t q4_layer_workspace(int P, int H, int I);
+int run_q4_layer(const Q4LayerArgs& a, hipStream_t st);
+int run_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, hipStream_t st);
+int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
+                float* out, int ldo, int H, hipStream_t st);
+
+}  // namespace moe

@@ -1,0 +1,55 @@
+// Internal interface of the decode mat-vec (matvec.hip), used by the exported
+// entry points in abi.hip.
+#pragma once
+#include "common.h"
+
+namespace moe {
+
+enum { FMT_Q4 = 0, FMT_Q8 = 1, FMT_Q8_0 = 8, FMT_Q4_K = 12 };  // GGUF ids as ggml's
+
+// One int4 expert as the fused layer call reads it; the layout of
+// moe_q4_expert in include/moehip.h.
+struct ExpertDesc {
+  const uint8_t* gu_w;  // gate|up bytes [2I, H/2]
+  const void* gu_s;     // their scales [2I, H/gs]
+  const uint8_t* dn_w;  // down bytes [H, I/2]
+  const void* dn_s;     // their scales [H, I/gs]
+  uint32_t xor8;        // 0x88: two's-complement nibbles as stored; 0: already XOR-ed
+  int32_t s_f16;        // scales are f16 (else f32)
+};
+
+struct MatRef {
+  const uint8_t* w;
+  const void* s;
+  uint32_t xor4;  // XOR for each 32-bit weight word
+  int s_f16;
+};
+
+struct MVShape {
+  int O, I;       // output rows, input columns
+  int gs, G;      // group size, groups per row (Q4/Q8)
+  int row_bytes;  // bytes per weight row
+  int cpr, rpp;   // chunks per row, rows per pass of a block
+  int pow2;       // cpr is a power of two <= 64 (cross-lane reduction)
+};
+
+struct MVJob {
+  const float* x;
+  int ldx;
+  float* y;
+  int ldy;
+  const int* seg;   // [nmat+1]: pairs of matrix m are seg[m]..seg[m+1]; null: pairs 0..n-1
+  const int* xrow;  // input row of each pair; null: the pair index itself
+  int n;
+  const ExpertDesc* experts;  // expert descriptors; null: `single`
+  const int* eidx;            // matrix m reads experts[eidx[m]]; null: experts[m]
+  MatRef single;
+  int which;    // 0: gate|up of the descriptor, 1: down
+  int half_in;  // > 0: input rows are h = gate|up (2*half_in wide), use silu(gate)*up
+};
+
+int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh);
+// y[pair] = x[xrow[pair]] @ W_m.T for every matrix m and its pairs
+int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st);
+
+}  // namespace moe

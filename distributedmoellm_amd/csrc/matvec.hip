@@ -1,0 +1,362 @@
+// Decode mat-vec y = x @ W.T straight from packed weight bytes, f32 accumulate.
+//
+// Replaces the numba kernels _q4 / _q4_rows / _q8 / _q8_rows / _mv_q8_0 /
+// _mv_q4_k / _gguf_mm (moelan/kernels.py:85-168, 482-527, 678-691) and the
+// gate|up and down sweeps of _moe_q4 (moelan/kernels.py:712-777).
+//
+// Work decomposition (one launch may cover many matrices, e.g. a layer's experts):
+//   grid.y  = matrix (expert), grid.x = tile of output rows of that matrix
+//   block   = rpp rows x cpr chunk columns; thread t owns chunk column t % cpr
+//             and row slot t / cpr, so one pass of the block reads rpp whole
+//             consecutive rows: contiguous, 16-byte loads per lane.
+//   PASSES  passes per block, all loads issued before any math.
+//   NR      input rows held in registers at once; more rows loop in batches
+//           (the tile's weights are re-read from L2, not HBM).
+// A lane computes sum(chunk of weights * chunk of x) * group scale; partial
+// sums of a row are added across its cpr lanes with cross-lane shuffles when
+// cpr is a power of two <= 64, else through LDS.
+#include "common.h"
+#include "formats.h"
+#include "matvec.h"
+
+namespace moe {
+
+// 16 weight bytes of a row: one 128-bit load when the matrix is 16-byte
+// aligned (the usual case: HBM buffers), byte loads otherwise.
+__device__ __forceinline__ uint4 load16(const uint8_t* p, bool a16) {
+  if (a16) return stream_load16(p);
+  uint32_t v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    v[i] = p[4 * i] | (p[4 * i + 1] << 8) | (p[4 * i + 2] << 16) | ((uint32_t)p[4 * i + 3] << 24);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ MatRef resolve(const MVJob& job, int mat) {
+  if (job.experts == nullptr) return job.single;
+  const ExpertDesc& e = job.experts[job.eidx ? job.eidx[mat] : mat];
+  MatRef m;
+  m.w = job.which ? e.dn_w : e.gu_w;
+  m.s = job.which ? e.dn_s : e.gu_s;
+  m.xor4 = e.xor8 * 0x01010101u;
+  m.s_f16 = e.s_f16;
+  return m;
+}
+
+// Adds the partials of a pass and writes y; `acc` is [PASSES][NR].
+template <int PASSES, int NR>
+__device__ __forceinline__ void reduce_store(const MVShape& sh, const MVJob& job, float (&acc)[PASSES][NR],
+                                             int row0, int rs, int c, int pb, int p1, float* red) {
+  const int t = threadIdx.x;
+  if (sh.pow2) {
+#pragma unroll
+    for (int k = 0; k < PASSES; ++k)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const float v = group_sum(acc[k][r], sh.cpr);
+        const int o = row0 + k * sh.rpp + rs;
+        if (c == 0 && rs < sh.rpp && o < sh.O && pb + r < p1) job.y[(size_t)(pb + r) * job.ldy + o] = v;
+      }
+    return;
+  }
+  const int ld = sh.cpr + 1;
+  if (rs < sh.rpp) {
+#pragma unroll
+    for (int k = 0; k < PASSES; ++k)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) red[((k * NR + r) * sh.rpp + rs) * ld + c] = acc[k][r];
+  }
+  __syncthreads();
+  const int nsum = PASSES * NR * sh.rpp;
+  for (int i = t; i < nsum; i += blockDim.x) {
+    const int rs2 = i % sh.rpp, kr = i / sh.rpp, r = kr % NR, k = kr / NR;
+    const float* p = red + i * ld;
+    float v = 0.f;
+    for (int j = 0; j < sh.cpr; ++j) v += p[j];
+    const int o = row0 + k * sh.rpp + rs2;
+    if (o < sh.O && pb + r < p1) job.y[(size_t)(pb + r) * job.ldy + o] = v;
+  }
+  __syncthreads();
+}
+
+template <class F, int NR, int PASSES>
+__global__ __launch_bounds__(256) void mv_kernel(MVShape sh, MVJob job) {
+  extern __shared__ float red[];
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  if (p0 >= p1) return;
+  const MatRef M = resolve(job, mat);
+  const int t = threadIdx.x;
+  const int c = t % sh.cpr, rs = t / sh.cpr;
+  const bool lane_on = rs < sh.rpp;
+  const int row0 = blockIdx.x * sh.rpp * PASSES;
+
+  const bool a16 = aligned(M.w, 16);
+  for (int pb = p0; pb < p1; pb += NR) {
+    float xr[NR][F::XR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (lane_on && pb + r < p1) {
+        const int p = pb + r;
+        const int xrow = job.xrow ? job.xrow[p] : p;
+        XSrc xs{job.x + (size_t)xrow * job.ldx, job.half_in};
+        F::load_x(xs, c, xr[r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < F::XR; ++j) xr[r][j] = 0.f;
+      }
+    }
+    uint4 w[PASSES];
+#pragma unroll
+    for (int k = 0; k < PASSES; ++k) {
+      const int o = row0 + k * sh.rpp + rs;
+      if (lane_on && o < sh.O) w[k] = load16(M.w + (size_t)o * sh.row_bytes + (size_t)c * 16, a16);
+      else w[k] = uint4{};
+    }
+    float acc[PASSES][NR];
+#pragma unroll
+    for (int k = 0; k < PASSES; ++k) {
+      const int o = row0 + k * sh.rpp + rs;
+      const bool on = lane_on && o < sh.O;
+      const float sc = on ? load_scale(M.s, (size_t)o * sh.G + (c * F::VALS) / sh.gs, M.s_f16) : 0.f;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) acc[k][r] = on ? F::dot(w[k], M.xor4, xr[r]) * sc : 0.f;
+    }
+    reduce_store<PASSES, NR>(sh, job, acc, row0, rs, c, pb, p1, red);
+  }
+}
+
+// GGUF: the block scale lives in the weight bytes, so the chunk is handled by
+// the format's own routine.
+template <class F, int NR, int PASSES>
+__global__ __launch_bounds__(256) void mv_gguf_kernel(MVShape sh, MVJob job) {
+  extern __shared__ float red[];
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  if (p0 >= p1) return;
+  const MatRef M = resolve(job, mat);
+  const int t = threadIdx.x;
+  const int c = t % sh.cpr, rs = t / sh.cpr;
+  const bool lane_on = rs < sh.rpp;
+  const int row0 = blockIdx.x * sh.rpp * PASSES;
+  const bool a16 = aligned(M.w, 16), a4 = aligned(M.w, 4) && sh.row_bytes % 4 == 0;
+
+  for (int pb = p0; pb < p1; pb += NR) {
+    float xr[NR][F::XR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (lane_on && pb + r < p1) {
+        const int p = pb + r;
+        const int xrow = job.xrow ? job.xrow[p] : p;
+        XSrc xs{job.x + (size_t)xrow * job.ldx, job.half_in};
+        F::load_x(xs, c, xr[r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < F::XR; ++j) xr[r][j] = 0.f;
+      }
+    }
+    float acc[PASSES][NR];
+    if constexpr (F::BYTES == 34) {
+#pragma unroll
+      for (int k = 0; k < PASSES; ++k) {
+        const int o = row0 + k * sh.rpp + rs;
+        const bool on = lane_on && o < sh.O;
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          acc[k][r] = on ? F::block_dot(M.w + (size_t)o * sh.row_bytes, c, xr[r], a4) : 0.f;
+      }
+    } else {
+      uint4 hdr[PASSES], q[PASSES];
+      const int sb = c >> 3;
+#pragma unroll
+      for (int k = 0; k < PASSES; ++k) {
+        const int o = row0 + k * sh.rpp + rs;
+        if (lane_on && o < sh.O) {
+          const uint8_t* blk = M.w + (size_t)o * sh.row_bytes + (size_t)sb * 144;
+          hdr[k] = load16(blk, a16);
+          q[k] = load16(blk + 16 + 16 * (c & 7), a16);
+        } else {
+          hdr[k] = uint4{};
+          q[k] = uint4{};
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < PASSES; ++k) {
+        const int o = row0 + k * sh.rpp + rs;
+        const bool on = lane_on && o < sh.O;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[k][r] = on ? F::dot(hdr[k], q[k], c, xr[r]) : 0.f;
+      }
+    }
+    reduce_store<PASSES, NR>(sh, job, acc, row0, rs, c, pb, p1, red);
+  }
+}
+
+// Any shape the chunked kernels do not take (group sizes that split a chunk,
+// unaligned rows): one thread per (output row, input row), straight loops.
+__global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  const MatRef M = resolve(job, mat);
+  const int np = p1 - p0;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < (long)np * sh.O; i += (long)gridDim.x * blockDim.x) {
+    const int p = p0 + (int)(i / sh.O), o = (int)(i % sh.O);
+    const int xrow = job.xrow ? job.xrow[p] : p;
+    XSrc xs{job.x + (size_t)xrow * job.ldx, job.half_in};
+    const uint8_t* row = M.w + (size_t)o * sh.row_bytes;
+    float acc = 0.f;
+    if (fmt == FMT_Q4) {
+      for (int g = 0; g < sh.G; ++g) {
+        float part = 0.f;
+        for (int j = 0; j < sh.gs; ++j) {
+          const int col = g * sh.gs + j;
+          const uint32_t b = row[col >> 1] ^ (M.xor4 & 0xFFu);
+          const int u = (col & 1) ? (int)(b >> 4) : (int)(b & 15u);
+          part = fmaf((float)(u - 8), xs(col), part);
+        }
+        acc = fmaf(part, load_scale(M.s, (size_t)o * sh.G + g, M.s_f16), acc);
+      }
+    } else if (fmt == FMT_Q8) {
+      for (int g = 0; g < sh.G; ++g) {
+        float part = 0.f;
+        for (int j = 0; j < sh.gs; ++j) {
+          const int col = g * sh.gs + j;
+          part = fmaf((float)(int8_t)row[col], xs(col), part);
+        }
+        acc = fmaf(part, load_scale(M.s, (size_t)o * sh.G + g, M.s_f16), acc);
+      }
+    } else if (fmt == FMT_Q8_0) {
+      for (int b = 0; b < sh.I / 32; ++b) {
+        const uint8_t* blk = row + 34 * b;
+        const float d = gguf_half(blk[0] | (blk[1] << 8));
+        float s = 0.f;
+        for (int j = 0; j < 32; ++j) s = fmaf((float)(int8_t)blk[2 + j], xs(b * 32 + j), s);
+        acc = fmaf(d, s, acc);
+      }
+    } else {  // Q4_K
+      for (int b = 0; b < sh.I / 256; ++b) {
+        const uint8_t* blk = row + 144 * b;
+        const float d = gguf_half(blk[0] | (blk[1] << 8)), dmin = gguf_half(blk[2] | (blk[3] << 8));
+        for (int kk = 0; kk < 4; ++kk) {
+          int sc1, m1, sc2, m2;
+          const FmtQ4K::MemBytes sb{blk + 4};
+          FmtQ4K::scale_min(2 * kk, sb, sc1, m1);
+          FmtQ4K::scale_min(2 * kk + 1, sb, sc2, m2);
+          float s1 = 0.f, s2 = 0.f, x1 = 0.f, x2 = 0.f;
+          for (int l = 0; l < 32; ++l) {
+            const uint32_t v = blk[16 + 32 * kk + l];
+            const float xa = xs(b * 256 + kk * 64 + l), xb = xs(b * 256 + kk * 64 + 32 + l);
+            s1 = fmaf((float)(v & 15u), xa, s1);
+            s2 = fmaf((float)(v >> 4), xb, s2);
+            x1 += xa;
+            x2 += xb;
+          }
+          acc += d * ((float)sc1 * s1 + (float)sc2 * s2) - dmin * ((float)m1 * x1 + (float)m2 * x2);
+        }
+      }
+    }
+    job.y[(size_t)p * job.ldy + o] = acc;
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+static int bytes_per_row(int fmt, int I) {
+  switch (fmt) {
+    case FMT_Q4: return I / 2;
+    case FMT_Q8: return I;
+    case FMT_Q8_0: return I / 32 * 34;
+    case FMT_Q4_K: return I / 256 * 144;
+  }
+  return 0;
+}
+
+static int vals_per_chunk(int fmt) {
+  switch (fmt) {
+    case FMT_Q4: return 32;
+    case FMT_Q8: return 16;
+    case FMT_Q8_0: return 32;
+    case FMT_Q4_K: return 32;
+  }
+  return 0;
+}
+
+int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh) {
+  sh->O = O;
+  sh->I = I;
+  sh->gs = gs;
+  sh->G = (fmt == FMT_Q4 || fmt == FMT_Q8) ? I / gs : 0;
+  sh->row_bytes = bytes_per_row(fmt, I);
+  const int v = vals_per_chunk(fmt);
+  sh->cpr = I / v;
+  sh->rpp = sh->cpr >= 256 ? 1 : 256 / sh->cpr;
+  sh->pow2 = (sh->cpr <= 64 && (sh->cpr & (sh->cpr - 1)) == 0) ? 1 : 0;
+  return MOE_OK;
+}
+
+// Whether the chunked kernels take this shape (pointer alignment is handled
+// inside them).
+static bool chunked_ok(int fmt, const MVShape& sh) {
+  if (sh.cpr < 1 || sh.cpr > 256) return false;
+  switch (fmt) {
+    case FMT_Q4: return sh.I % 32 == 0 && sh.gs % 32 == 0 && sh.row_bytes % 16 == 0;
+    case FMT_Q8: return sh.I % 16 == 0 && sh.gs % 16 == 0 && sh.row_bytes % 16 == 0;
+    case FMT_Q8_0: return sh.I % 32 == 0;
+    case FMT_Q4_K: return sh.I % 256 == 0;
+  }
+  return false;
+}
+
+template <class F, int NR, int PASSES>
+static void launch_nr(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st) {
+  const int rows_per_block = sh.rpp * PASSES;
+  dim3 grid((sh.O + rows_per_block - 1) / rows_per_block, nmat);
+  dim3 block(sh.rpp * sh.cpr);
+  const size_t lds = sh.pow2 ? 0 : (size_t)PASSES * NR * sh.rpp * (sh.cpr + 1) * sizeof(float);
+  if constexpr (F::GGUF) hipLaunchKernelGGL((mv_gguf_kernel<F, NR, PASSES>), grid, block, lds, st, sh, job);
+  else hipLaunchKernelGGL((mv_kernel<F, NR, PASSES>), grid, block, lds, st, sh, job);
+}
+
+template <class F>
+static void launch_fmt(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
+  constexpr int P = 4;
+  if (max_rows <= 1) launch_nr<F, 1, P>(sh, job, nmat, st);
+  else if (max_rows <= 2) launch_nr<F, 2, P>(sh, job, nmat, st);
+  else launch_nr<F, 4, P>(sh, job, nmat, st);
+}
+
+int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
+  if (max_rows <= 0 || nmat <= 0 || sh.O <= 0) return MOE_OK;
+  if (chunked_ok(fmt, sh)) {
+    const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
+    const size_t lds = sh.pow2 ? 0 : (size_t)4 * nr * sh.rpp * (sh.cpr + 1) * sizeof(float);
+    if (lds <= 64 * 1024) {
+      switch (fmt) {
+        case FMT_Q4: launch_fmt<FmtQ4>(sh, job, nmat, max_rows, st); break;
+        case FMT_Q8: launch_fmt<FmtQ8>(sh, job, nmat, max_rows, st); break;
+        case FMT_Q8_0: launch_fmt<FmtQ8_0>(sh, job, nmat, max_rows, st); break;
+        case FMT_Q4_K: launch_fmt<FmtQ4K>(sh, job, nmat, max_rows, st); break;
+      }
+      return check_launch("decode mat-vec");
+    }
+  }
+  const long work = (long)max_rows * sh.O;
+  const int threads = 256;
+  const int blocks = (int)((work + threads - 1) / threads > 4096 ? 4096 : (work + threads - 1) / threads);
+  hipLaunchKernelGGL(mv_generic_kernel, dim3(blocks, nmat), dim3(threads), 0, st, sh, job, fmt, nmat);
+  return check_launch("decode mat-vec (generic)");
+}
+
+}  // namespace moe

@@ -1,0 +1,249 @@
+"""Expert matrices and the expert store, resident in HBM.
+
+Mirrors the matrix protocol and expert classes of ``moelan/experts.py``
+(``matmul_t(x) == x @ W.T``, ``dequant()``, ``nbytes``: 66-69; ``GroupQuant``
+125-167, ``Packed4`` 170-236, ``Expert`` 247-263, ``ExpertStore.compute``
+641-670) with every product computed by the HIP kernels of
+:mod:`distributedmoellm_amd.kernels`. A matrix keeps what it was given
+(numpy, possibly a read-only memory map, or a device tensor) and uploads one
+device copy on first use, which it keeps: packed bytes and scales stay
+resident in HBM and are never widened to a full-precision copy.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import kernels
+
+FORMATS = ("int8", "int4", "native")
+
+
+def _dev_or_none(a):
+    return a if kernels.is_device(a) else None
+
+
+class GroupQuant:
+    """int8 values with one f32 (or f16) scale per ``gs`` inputs of each output row."""
+
+    __slots__ = ("q", "s", "gs", "_dev")
+
+    def __init__(self, q, s, gs: int):
+        self.q, self.s, self.gs = q, s, gs
+        self._dev = None
+
+    @classmethod
+    def quantize(cls, w: np.ndarray, gs: int = 64) -> "GroupQuant":
+        """moelan/experts.py:133-142 (host-side, load time)."""
+        O, I = w.shape
+        if I % gs:
+            gs = I
+        g = w.reshape(O, I // gs, gs)
+        amax = np.abs(g).max(axis=2)
+        s = np.where(amax == 0, 1.0, amax / 127.0).astype(np.float32)
+        q = np.clip(np.rint(g / s[:, :, None]), -127, 127).astype(np.int8).reshape(O, I)
+        return cls(q, s, gs)
+
+    def device_arrays(self):
+        if self._dev is None:
+            import torch
+            O, I = self.q.shape
+            self._dev = (kernels.to_device(self.q, torch.int8).reshape(O, I),
+                         kernels.to_device(self.s).reshape(O, I // self.gs))
+        return self._dev
+
+    @property
+    def shape(self):
+        return tuple(self.q.shape)
+
+    def dequant(self):
+        import torch
+        q, s = self.device_arrays()
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        kernels.q8_dequant(q, s, self.gs, out)
+        return out if _dev_or_none(self.q) is not None else out.cpu().numpy()
+
+    def matmul_t(self, x):
+        q, s = self.device_arrays()
+        return kernels.q8_matmul_t(x, q, s, self.gs)
+
+    @property
+    def nbytes(self):
+        return int(self.q.nbytes + self.s.nbytes)
+
+
+class Packed4:
+    """Colibri's int4: two signed 4-bit values per byte (low nibble = even
+    column), one scale per ``gs`` inputs; ``offset`` means the bytes were XOR-ed
+    with 0x88 once (resident copies), so nibbles read as u = v + 8."""
+
+    __slots__ = ("raw", "s", "gs", "shape", "offset", "_dev")
+
+    def __init__(self, raw, s, gs: int, shape: tuple[int, int], offset: bool = False):
+        self.raw, self.s, self.gs, self.shape, self.offset = raw, s, gs, tuple(shape), offset
+        self._dev = None
+
+    def device_arrays(self):
+        """(raw uint8 [O, I/2], scales [O, I/gs]) on the device, uploaded once."""
+        if self._dev is None:
+            import torch
+            O, I = self.shape
+            self._dev = (kernels.to_device(self.raw, torch.uint8).reshape(O, I // 2),
+                         kernels.to_device(self.s).reshape(O, I // self.gs))
+        return self._dev
+
+    def resident(self) -> "Packed4":
+        """A copy in offset form (moelan/experts.py:188-191), XOR-ed once on the
+        host at load time and uploaded."""
+        raw = self.raw.cpu().numpy() if kernels.is_device(self.raw) else np.asarray(self.raw)
+        s = self.s.cpu().numpy() if kernels.is_device(self.s) else np.array(self.s)
+        raw = np.ascontiguousarray(raw if self.offset else np.bitwise_xor(raw, 0x88))
+        p = Packed4(raw, s, self.gs, self.shape, True)
+        p.device_arrays()
+        return p
+
+    def to_int8(self) -> GroupQuant:
+        """int8 values v = u - 8 with the same scales (moelan/experts.py:205-211); load-time, on the host."""
+        raw = self.raw.cpu().numpy() if kernels.is_device(self.raw) else np.asarray(self.raw)
+        rr = raw if self.offset else np.bitwise_xor(raw, 0x88)
+        O, I = self.shape
+        u = np.empty((O, I // 2, 2), np.int16)
+        u[:, :, 0] = rr.reshape(O, I // 2) & 15
+        u[:, :, 1] = rr.reshape(O, I // 2) >> 4
+        s = self.s.cpu().numpy() if kernels.is_device(self.s) else np.array(self.s)
+        return GroupQuant((u.reshape(O, I) - 8).astype(np.int8), s, self.gs)
+
+    def dequant(self):
+        import torch
+        raw, s = self.device_arrays()
+        out = torch.empty(self.shape, dtype=torch.float32, device=raw.device)
+        kernels.q4_dequant(raw, s, self.gs, self.offset, out)
+        return out if _dev_or_none(self.raw) is not None else out.cpu().numpy()
+
+    def matmul_t(self, x):
+        raw, s = self.device_arrays()
+        return kernels.q4_matmul_t(x, raw, s, self.gs, self.offset)
+
+    @property
+    def nbytes(self):
+        return int(self.raw.nbytes + self.s.nbytes)
+
+
+class Expert:
+    """A SwiGLU expert with gate and up fused into one (2*inter, hidden) matrix
+    (moelan/experts.py:247-263)."""
+
+    __slots__ = ("gu", "down", "inter", "fused")
+
+    def __init__(self, gu, down, inter: int):
+        self.gu, self.down, self.inter = gu, down, inter
+        self.fused = None   # q4_expert_ptrs() once asked (False: not that kind)
+
+    def __call__(self, x):
+        """down(silu(gate(x)) * up(x)); int4 experts run as one fused layer call."""
+        import torch
+        if isinstance(self.gu, Packed4) and isinstance(self.down, Packed4):
+            ptrs = kernels.q4_expert_ptrs(self)
+            if ptrs is not None:
+                xd = kernels.to_device(x, torch.float32)
+                n, H = xd.shape
+                out = torch.zeros((n, H), dtype=torch.float32, device=xd.device)
+                rows = np.arange(n, dtype=np.int32)
+                kernels.moe_q4(xd, [(ptrs, rows, np.ones(n, np.float32))], H, self.inter, self.gu.gs, out)
+                return out if kernels.is_device(x) else out.cpu().numpy()
+        h = self.gu.matmul_t(kernels.to_device(x, torch.float32))
+        a = silu_mul(h, self.inter)
+        y = self.down.matmul_t(a)
+        return y if kernels.is_device(x) else y.cpu().numpy()
+
+    @property
+    def nbytes(self):
+        return self.gu.nbytes + self.down.nbytes
+
+
+def silu_mul(h, inter: int):
+    """silu(h[:, :inter]) * h[:, inter:] on the device (HIP kernel)."""
+    import torch
+    from . import _lib
+    hd = kernels.to_device(h, torch.float32)
+    n = hd.shape[0]
+    a = torch.empty((n, inter), dtype=torch.float32, device=hd.device)
+    _lib.call("moe_silu_mul", hd.data_ptr(), hd.shape[1], n, inter, a.data_ptr(), inter, kernels.stream_handle())
+    return a
+
+
+def synthetic_expert(hidden: int, inter: int, fmt: str, gs: int = 32, rng=None, scale_dtype=np.float16) -> Expert:
+    """A random expert of the given shape (host arrays), drawn as the benchmark
+    configurations say: int4 nibbles uniform, scales |N(0,0.02)|/8; int8 uniform
+    in [-127, 127], scales |N(0,0.02)|/127 (cf. moelan/experts.py:322-339)."""
+    rng = rng or np.random.default_rng(0)
+
+    def mat(o, i):
+        if fmt == "int4":
+            raw = rng.integers(0, 256, (o, i // 2), dtype=np.uint8)
+            s = (np.abs(rng.normal(0.0, 0.02, (o, i // gs))) / 8).astype(scale_dtype)
+            return Packed4(raw, s, gs, (o, i))
+        if fmt == "int8":
+            q = rng.integers(-127, 128, (o, i), dtype=np.int8)
+            s = (np.abs(rng.normal(0.0, 0.02, (o, i // gs))) / 127).astype(scale_dtype)
+            return GroupQuant(q, s, gs)
+        raise ValueError(f"unknown expert format {fmt!r}")
+    return Expert(mat(2 * inter, hidden), mat(hidden, inter), inter)
+
+
+class ExpertStore:
+    """Resident experts by (layer, expert) and the per-layer compute call
+    (moelan/experts.py:538-670, the compute path only: no disk tiers)."""
+
+    def __init__(self, experts: dict | None = None, fmt: str = "int4"):
+        if fmt not in FORMATS:
+            raise ValueError(f"format must be one of {FORMATS}")
+        self.fmt = fmt
+        self.pinned: dict = dict(experts or {})
+        self.hits = 0
+        self.misses = 0
+
+    def pin(self, items) -> None:
+        """Add experts ((layer, expert), Expert) and upload their arrays now."""
+        for key, e in items:
+            for m in (e.gu, e.down):
+                for part in getattr(m, "parts", (m,)):
+                    if hasattr(part, "device_arrays"):
+                        part.device_arrays()
+            self.pinned[tuple(key)] = e
+
+    def get(self, key):
+        e = self.pinned.get(tuple(key))
+        if e is None:
+            raise KeyError(f"expert {key} is not resident")
+        self.hits += 1
+        return e
+
+    def compute(self, layer: int, x, groups):
+        """Weighted sum of the routed experts' outputs for the given rows.
+        ``groups``: (expert, rows, weights) per expert. int4 experts run in one
+        fused layer call; others one after another. Returns the type of ``x``."""
+        import torch
+        groups = list(groups)
+        xd = kernels.to_device(x, torch.float32)
+        out = torch.zeros(xd.shape, dtype=torch.float32, device=xd.device)
+        items, H, shape = [], xd.shape[1], None
+        ys, yrows, yw = [], [], []
+        for expert, rows, weights in groups:
+            e = self.get((layer, int(expert)))
+            if kernels.FUSED and e.fused is None:
+                ok = isinstance(e.gu, Packed4) and isinstance(e.down, Packed4)
+                e.fused = (kernels.q4_expert_ptrs(e) if ok else None) or False
+            dims = (e.inter, e.gu.gs) if e.fused else None
+            if kernels.FUSED and e.fused and (shape is None or dims == shape):
+                shape = dims
+                items.append((e.fused, rows, weights))
+                continue
+            rows_t = torch.as_tensor(np.asarray(rows, np.int64), device=xd.device)
+            ys.append(e(xd.index_select(0, rows_t)))
+            yrows.append(rows)
+            yw.append(weights)
+        kernels.combine(out, ys, yrows, yw)
+        if items:
+            kernels.moe_q4(xd, items, H, shape[0], shape[1], out)
+        return out if kernels.is_device(x) else out.cpu().numpy()

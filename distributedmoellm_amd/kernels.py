@@ -1,0 +1,359 @@
+"""The compute kernels of moelan's routed-expert path, on an MI355X.
+
+Same module surface as ``moelan/kernels.py`` (flags 19-32, functions 920-1032)
+so that ``experts.py`` / ``gguf.py`` style callers can select it as their
+backend; every function runs hand-written HIP kernels (libmoehip.so, C ABI in
+include/moehip.h) on the current ROCm device.
+
+Arrays may be numpy (host: copied to the device for the call, results copied
+back, as a drop-in) or torch tensors already on the device (no copies; the
+result stays on the device). There is no CPU fallback: without the library or
+a GPU ``ENABLED`` is False, ``WHY_DISABLED`` says why, and every kernel call
+raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+import warnings
+
+import numpy as np
+
+from . import _lib
+
+ENABLED = False
+WHY_DISABLED = ""
+MAX_ROWS = 1 << 30          # every size runs on the device
+ROW_DECODE_FROM = 4         # kept for callers that split on it (moelan/kernels.py:22)
+BLAS_FROM = 8               # idem (moelan/kernels.py:23): the store sends such groups to the big-group path
+FUSED = os.environ.get("MOELAN_FUSED", "1") != "0"
+INT8_ACT = False            # the int8-activation variant of moe_q4 is not provided
+AVX2 = False
+
+try:
+    import torch
+except ImportError:  # pragma: no cover - torch is part of the image
+    torch = None
+
+if os.environ.get("MOELAN_KERNELS", "1") == "0":
+    WHY_DISABLED = "MOELAN_KERNELS=0"
+elif torch is None:
+    WHY_DISABLED = "torch is not importable"
+elif _lib.load() is None:
+    WHY_DISABLED = _lib.why_not()
+elif _lib.lib().moe_device_count() < 1 or not torch.cuda.is_available():
+    WHY_DISABLED = "no HIP device is visible"
+else:
+    _rc = _lib.lib().moe_init(torch.cuda.current_device())
+    if _rc == 0:
+        ENABLED = True
+    else:
+        WHY_DISABLED = _lib.last_error()
+
+
+def warn_if_slow(stream=None) -> bool:
+    """Print a loud notice when the HIP kernels are off. Returns True if so."""
+    if ENABLED:
+        return False
+    stream = stream or sys.stderr
+    bar = "!" * 78
+    print(f"{bar}\n moelan's HIP expert kernels are OFF ({WHY_DISABLED}).\n"
+          f" The routed-expert path cannot run on this machine.\n{bar}", file=stream, flush=True)
+    return True
+
+
+def _need() -> None:
+    if not ENABLED:
+        raise RuntimeError(f"HIP expert kernels are not available: {WHY_DISABLED}")
+
+
+# ---------------------------------------------------------------- buffers
+
+def device():
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def stream_handle() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def is_device(a) -> bool:
+    return torch is not None and isinstance(a, torch.Tensor) and a.is_cuda
+
+
+def to_device(a, dtype=None):
+    """A contiguous device tensor with the contents of ``a`` (numpy or torch)."""
+    if isinstance(a, torch.Tensor):
+        t = a if a.is_cuda else a.to(device())
+    else:
+        arr = np.ascontiguousarray(a)
+        with warnings.catch_warnings():   # read-only memory maps: only read for the copy
+            warnings.simplefilter("ignore")
+            t = torch.from_numpy(arr)
+        t = t.to(device())
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def _f32(x):
+    return to_device(x, torch.float32)
+
+
+def _scale_kind(s) -> int:
+    dt = s.dtype if isinstance(s, torch.Tensor) else np.dtype(s.dtype)
+    if dt in (torch.float16, np.float16):
+        return 1
+    if dt in (torch.float32, np.float32):
+        return 0
+    raise TypeError(f"scales must be float32 or float16, not {dt}")
+
+
+def _ret(y, like):
+    """Results leave as they came: device tensors stay, numpy callers get numpy."""
+    return y if is_device(like) else y.cpu().numpy()
+
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+# ---------------------------------------------------------------- one matrix
+
+def q4_matmul_t(x, raw, s, gs: int, offset: bool):
+    """x @ W.T for colibri int4 bytes; ``offset`` means raw was XOR-ed with 0x88."""
+    _need()
+    xd = _f32(x)
+    if xd.dim() != 2:
+        raise ValueError("x must be 2-D (rows, columns)")
+    rd, sd = to_device(raw, torch.uint8), to_device(s)
+    n, I = xd.shape
+    O = rd.shape[0]
+    if rd.numel() != O * (I // 2) or sd.numel() != O * (I // gs):
+        raise ValueError(f"int4 matrix of {tuple(rd.shape)} bytes / {tuple(sd.shape)} scales does not match x {tuple(xd.shape)}, gs={gs}")
+    y = torch.empty((n, O), dtype=torch.float32, device=xd.device)
+    _lib.call("moe_q4_matmul_t", _ptr(xd), n, _ptr(rd), _ptr(sd), _scale_kind(sd), O, I, gs,
+              1 if offset else 0, _ptr(y), stream_handle())
+    return _ret(y, x)
+
+
+def q8_matmul_t(x, q, s, gs: int):
+    _need()
+    xd = _f32(x)
+    qd, sd = to_device(q, torch.int8), to_device(s)
+    n, I = xd.shape
+    O = qd.shape[0]
+    if qd.numel() != O * I or sd.numel() != O * (I // gs):
+        raise ValueError(f"int8 matrix {tuple(qd.shape)} / scales {tuple(sd.shape)} does not match x {tuple(xd.shape)}")
+    y = torch.empty((n, O), dtype=torch.float32, device=xd.device)
+    _lib.call("moe_q8_matmul_t", _ptr(xd), n, _ptr(qd), _ptr(sd), _scale_kind(sd), O, I, gs, _ptr(y),
+              stream_handle())
+    return _ret(y, x)
+
+
+def gguf_matmul_t(x, raw, qtype: int, cols: int):
+    """x @ W.T for a GGUF block-quantized W given as (rows, row bytes)."""
+    _need()
+    xd = _f32(x)
+    rd = to_device(raw, torch.uint8)
+    n = xd.shape[0]
+    O = rd.shape[0]
+    _check_gguf(rd, qtype, cols)
+    if xd.shape[1] != cols:
+        raise ValueError(f"x has {xd.shape[1]} columns, the matrix {cols}")
+    y = torch.empty((n, O), dtype=torch.float32, device=xd.device)
+    _lib.call("moe_gguf_matmul_t", _ptr(xd), n, _ptr(rd), int(qtype), O, int(cols), _ptr(y), stream_handle())
+    return _ret(y, x)
+
+
+def _check_gguf(rd, qtype: int, cols: int) -> None:
+    blocks = {8: (32, 34), 12: (256, 144)}
+    if qtype not in blocks:
+        raise ValueError(f"GGUF type {qtype} is not supported (8 Q8_0, 12 Q4_K)")
+    per, size = blocks[qtype]
+    if cols % per or rd.numel() != rd.shape[0] * (cols // per) * size:
+        raise ValueError(f"GGUF rows of {rd.numel() // max(rd.shape[0], 1)} bytes do not hold {cols} type-{qtype} values")
+
+
+def _check_out(out, O: int, I: int) -> None:
+    if tuple(out.shape) != (O, I):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {(O, I)}")
+
+
+# ---------------------------------------------------------------- dequant
+
+def _into(out, y):
+    if is_device(out):
+        out.copy_(y.view(out.shape))
+    else:
+        out[...] = y.cpu().numpy().reshape(out.shape)
+    return out
+
+
+def q4_dequant(raw, s, gs: int, offset: bool, out):
+    _need()
+    rd, sd = to_device(raw, torch.uint8), to_device(s)
+    O, I = rd.shape[0], rd.numel() // rd.shape[0] * 2
+    _check_out(out, O, I)
+    if sd.numel() != O * (I // gs):
+        raise ValueError(f"{sd.numel()} scales for a {O}x{I} matrix with groups of {gs}")
+    y = out if (is_device(out) and out.is_contiguous() and out.dtype == torch.float32) else \
+        torch.empty((O, I), dtype=torch.float32, device=rd.device)
+    _lib.call("moe_q4_dequant", _ptr(rd), _ptr(sd), _scale_kind(sd), O, I, gs, 1 if offset else 0, _ptr(y),
+              stream_handle())
+    return out if y is out else _into(out, y)
+
+
+def q8_dequant(q, s, gs: int, out):
+    _need()
+    qd, sd = to_device(q, torch.int8), to_device(s)
+    O, I = qd.shape
+    _check_out(out, O, I)
+    if sd.numel() != O * (I // gs):
+        raise ValueError(f"{sd.numel()} scales for a {O}x{I} matrix with groups of {gs}")
+    y = out if (is_device(out) and out.is_contiguous() and out.dtype == torch.float32) else \
+        torch.empty((O, I), dtype=torch.float32, device=qd.device)
+    _lib.call("moe_q8_dequant", _ptr(qd), _ptr(sd), _scale_kind(sd), O, I, gs, _ptr(y), stream_handle())
+    return out if y is out else _into(out, y)
+
+
+def gguf_dequant(raw, qtype: int, out):
+    _need()
+    rd = to_device(raw, torch.uint8)
+    O, cols = out.shape
+    if rd.shape[0] != O:
+        raise ValueError(f"{rd.shape[0]} GGUF rows for an output of {O} rows")
+    _check_gguf(rd, qtype, cols)
+    y = out if (is_device(out) and out.is_contiguous() and out.dtype == torch.float32) else \
+        torch.empty((O, cols), dtype=torch.float32, device=rd.device)
+    _lib.call("moe_gguf_dequant", _ptr(rd), int(qtype), O, cols, _ptr(y), stream_handle())
+    return out if y is out else _into(out, y)
+
+
+# ---------------------------------------------------------------- one layer
+
+def int8_act_for(H: int, I: int, gs: int) -> bool:
+    """Whether moe_q4 would round activations to int8: never here (float activations, exact)."""
+    return False
+
+
+def q4_expert_ptrs(e):
+    """What :func:`moe_q4` needs of one int4 expert: the device addresses of its
+    four arrays, the XOR for its nibbles and whether its scales are f16; None if
+    it does not qualify (moelan/kernels.py:929-939)."""
+    gu, dn = e.gu, e.down
+    if not (hasattr(gu, "device_arrays") and hasattr(dn, "device_arrays")):
+        return None
+    if gu.gs != dn.gs or gu.offset != dn.offset:
+        return None
+    gr, gsc = gu.device_arrays()
+    dr, dsc = dn.device_arrays()
+    if gsc.dtype != dsc.dtype:
+        return None
+    return (gr.data_ptr(), gsc.data_ptr(), dr.data_ptr(), dsc.data_ptr(), 0 if gu.offset else 0x88,
+            1 if gsc.dtype == torch.float16 else 0)
+
+
+def pair_lists(rows, weights):
+    """(poff, prow, pw, rrow, rptr, rpair) of a layer call, host int32/f32 arrays:
+    pairs in item order, then the pairs of each touched row in ascending order."""
+    k = len(rows)
+    counts = np.array([len(r) for r in rows], np.int64)
+    P = int(counts.sum())
+    prow = np.concatenate([np.asarray(r, np.int64).reshape(-1) for r in rows]).astype(np.int32) if P else \
+        np.zeros(0, np.int32)
+    pw = np.concatenate([np.asarray(w, np.float32).reshape(-1) for w in weights]) if P else np.zeros(0, np.float32)
+    poff = np.zeros(k + 1, np.int32)
+    np.cumsum(counts, out=poff[1:])
+    order = np.argsort(prow, kind="stable")
+    rrow, starts = np.unique(prow[order], return_index=True)
+    rptr = np.append(starts, P).astype(np.int32)
+    return poff, prow, pw, rrow.astype(np.int32), rptr, order.astype(np.int32)
+
+
+def upload_parts(parts):
+    """Host byte strings into one device buffer (one copy), 256-byte aligned
+    parts; returns (buffer, [device address of each part])."""
+    offs, pos = [], 0
+    for b in parts:
+        offs.append(pos)
+        pos += (len(b) + 255) // 256 * 256
+    host = np.zeros(max(pos, 256), np.uint8)
+    for o, b in zip(offs, parts):
+        host[o:o + len(b)] = np.frombuffer(b, np.uint8)
+    buf = to_device(host)
+    base = buf.data_ptr()
+    return buf, [base + o for o in offs]
+
+
+def combine(out, ys, rows, weights) -> None:
+    """out[rows_i] += ys_i * weights_i for each i, per row in the given order
+    (HIP combine kernel); ``ys`` are device tensors [len(rows_i), H]."""
+    _need()
+    if not ys:
+        return
+    H = out.shape[1]
+    y = torch.cat([t.reshape(-1, H) for t in ys], 0).contiguous()
+    _, _, pw, rrow, rptr, rpair = pair_lists(rows, weights)
+    buf, (pw_p, rrow_p, rptr_p, rpair_p) = upload_parts([pw.tobytes(), rrow.tobytes(), rptr.tobytes(),
+                                                         rpair.tobytes()])
+    _lib.call("moe_combine", _ptr(y), H, pw_p, rrow_p, rptr_p, rpair_p, len(rrow), _ptr(out), out.shape[1], H,
+              stream_handle())
+
+
+class LayerMeta:
+    """A layer call's pair lists on the device, in one upload: the expert table,
+    pairs per expert (poff, prow, pw) and pairs per touched row (rrow, rptr, rpair)."""
+
+    def __init__(self, ptrs, rows, weights):
+        k = len(ptrs)
+        poff, prow, pw, rrow, rptr, rpair = pair_lists(rows, weights)
+        table = (_lib.Q4Expert * max(k, 1))()
+        for i, p in enumerate(ptrs):
+            table[i] = _lib.Q4Expert(p[0], p[1], p[2], p[3], p[4], p[5] if len(p) > 5 else 0)
+        self.ptrs = [tuple(p) for p in ptrs]
+        self.buf, addrs = upload_parts([bytes(table), poff.tobytes(), prow.tobytes(), pw.tobytes(), rrow.tobytes(),
+                                        rptr.tobytes(), rpair.tobytes()])
+        (self.table, self.poff, self.prow, self.pw, self.rrow, self.rptr, self.rpair) = addrs
+        counts = np.diff(poff)
+        self.k, self.P, self.nr = k, int(poff[-1]), len(rrow)
+        self.max_rows = int(counts.max()) if k else 0
+        self.row_hi = int(prow.max()) + 1 if self.P else 0   # rows of x / out the call touches
+        if self.P and int(prow.min()) < 0:
+            raise ValueError("negative row index")
+
+
+def moe_q4(x, items, H: int, I: int, gs: int, out) -> None:
+    """Add ``sum_e w * expert_e(x[rows])`` into ``out`` for int4 experts in one
+    call (moelan/kernels.py:942-968). ``items``: (ptrs from
+    :func:`q4_expert_ptrs`, rows, gate weights) per expert; the experts'
+    device arrays must stay alive until the call has run."""
+    _need()
+    if not items:
+        return
+    meta = LayerMeta([p for p, _, _ in items], [r for _, r, _ in items], [w for _, _, w in items])
+    moe_q4_run(x, meta, H, I, gs, out)
+
+
+def moe_q4_run(x, meta: LayerMeta, H: int, I: int, gs: int, out, workspace=None) -> None:
+    """The layer call on pair lists already on the device."""
+    _need()
+    xd = _f32(x)
+    od = out if (is_device(out) and out.dtype == torch.float32 and out.is_contiguous()) else _f32(out)
+    if xd.shape[1] != H or od.shape[1] != H:
+        raise ValueError(f"x and out need {H} columns, have {xd.shape[1]} and {od.shape[1]}")
+    if meta.row_hi > min(xd.shape[0], od.shape[0]):
+        raise ValueError(f"row {meta.row_hi - 1} is out of range for x/out of {xd.shape[0]}/{od.shape[0]} rows")
+    for p in meta.ptrs:
+        if not all(p[:4]):
+            raise ValueError("null expert address")
+    need = _lib.lib().moe_q4_layer_workspace(max(meta.P, 1), H, I)
+    ws = workspace if workspace is not None and workspace.numel() >= need else \
+        torch.empty(need, dtype=torch.uint8, device=xd.device)
+    _lib.call("moe_q4_layer", _ptr(xd), xd.shape[1], meta.table, None, meta.k, meta.poff, meta.prow, meta.pw,
+              meta.P, meta.rrow, meta.rptr, meta.rpair, meta.nr, _ptr(od), od.shape[1], H, I, gs,
+              meta.max_rows, _ptr(ws), ws.numel(), stream_handle())
+    if od is not out:
+        _into(out, od)

@@ -1,0 +1,135 @@
+/*
+ * moehip: MI355X (gfx950) routed-expert compute path of moelan, as a C ABI.
+ *
+ * Every pointer named a "device" pointer is HBM memory of the current HIP
+ * device (e.g. a torch tensor's data_ptr()); host pointers are marked as such.
+ * `stream` is a hipStream_t (NULL: the default stream). Calls are stream
+ * ordered and return before the GPU finishes. Every call returns 0 on success
+ * or a non-zero MOE_E* code, with a message in moe_last_error() (per thread).
+ * The library allocates nothing: scratch comes from the caller's workspace.
+ *
+ * Conventions shared with moelan (citations are files of the reference):
+ *   int4 "Packed4"  raw uint8 [O, I/2], byte j = column 2j (low nibble) and
+ *                   2j+1 (high nibble), two's-complement nibbles; offset != 0
+ *                   means the bytes were XOR-ed with 0x88 already (u = v + 8).
+ *                   Scales [O, I/gs], f32 or f16 (s_f16 != 0).
+ *                   moelan/experts.py:170-236, moelan/tiny.py:94-106
+ *   int8 "GroupQuant" q int8 [O, I], scales [O, I/gs]. moelan/experts.py:125-167
+ *   GGUF            raw uint8 [O, row bytes], qtype 8 (Q8_0) or 12 (Q4_K).
+ *                   moelan/gguf.py:36-42, moelan/kernels.py:262-336
+ */
+#ifndef MOEHIP_H
+#define MOEHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_EINVAL 1
+#define MOE_EHIP 2
+#define MOE_EWORKSPACE 3
+#define MOE_EUNSUPPORTED 4
+
+/* ---------------------------------------------------------------- library */
+
+/* Checks that `device` is usable (gfx950 class, MFMA present).
+ * Replaces the import-time probe that sets ENABLED / WHY_DISABLED,
+ * moelan/kernels.py:19-41. */
+int moe_init(int device);
+
+/* Message of the last failed call on this thread ("" if none).
+ * moelan/kernels.py:20 (WHY_DISABLED). */
+const char* moe_last_error(void);
+
+/* Number of visible HIP devices (0 without a GPU); never fails. */
+int moe_device_count(void);
+
+/* "name|arch|CUs|max clock kHz|HBM bytes" of `device` into buf. */
+int moe_device_info(int device, char* buf, int len);
+
+/* ABI version (major*100 + minor). */
+int moe_version(void);
+
+/* ------------------------------------------------------- one matrix: x @ W.T */
+
+/* y[n, O] = x[n, I] @ W.T for colibri int4 weights, f32 accumulate.
+ * Replaces q4_matmul_t(x, raw, s, gs, offset), moelan/kernels.py:1018-1027
+ * (kernels _q4 :85-106 and _q4_rows :108-131). x, raw, s, y: device. */
+int moe_q4_matmul_t(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs,
+                    int offset, float* y, void* stream);
+
+/* y[n, O] = x @ W.T for group-scaled int8 weights.
+ * Replaces q8_matmul_t(x, q, s, gs), moelan/kernels.py:1030-1032 (_q8 :152-168,
+ * _q8_rows :133-150). */
+int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* s, int s_f16, int O, int I, int gs,
+                    float* y, void* stream);
+
+/* y[n, O] = x[n, cols] @ W.T for GGUF block-quantized rows (qtype 8 or 12).
+ * Replaces gguf_matmul_t(x, raw, qtype, cols), moelan/kernels.py:981-998
+ * (_mv_q8_0 :482-497, _mv_q4_k :499-527, _gguf_mm :678-691). */
+int moe_gguf_matmul_t(const float* x, int n, const uint8_t* raw, int qtype, int O, int cols, float* y,
+                      void* stream);
+
+/* ---------------------------------------------------------------- dequant */
+
+/* out[O, I] f32 = (u - 8) * s, bit-exact.
+ * Replaces q4_dequant(raw, s, gs, offset, out), moelan/kernels.py:971-973. */
+int moe_q4_dequant(const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs, int offset, float* out,
+                   void* stream);
+
+/* out = q * s, bit-exact. Replaces q8_dequant, moelan/kernels.py:976-978. */
+int moe_q8_dequant(const int8_t* q, const void* s, int s_f16, int O, int I, int gs, float* out, void* stream);
+
+/* out[O, cols] f32 from GGUF rows, bit-exact with the reference decoders.
+ * Replaces gguf_dequant(raw, qtype, out), moelan/kernels.py:1001-1003. */
+int moe_gguf_dequant(const uint8_t* raw, int qtype, int O, int cols, float* out, void* stream);
+
+/* a[n, I] = silu(h[:, :I]) * h[:, I:] for h [n, 2I] (row strides ldh, lda).
+ * The middle of Expert.__call__, moelan/experts.py:256-259 (silu :62-63). */
+int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, void* stream);
+
+/* out[rrow[i]] += sum over q in rptr[i]..rptr[i+1] of pw[p] * y[p], p = rpair[q],
+ * the sum formed in that order first: the weighted combine of per-expert
+ * outputs, out[rows] += e(x[rows]) * w, moelan/experts.py:648-651, 707-727
+ * and moelan/kernels.py:778-782, 968. y [P, H] (stride ldy), out stride ldo. */
+int moe_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
+                float* out, int ldo, int H, void* stream);
+
+/* -------------------------------------------- one MoE layer, few rows each */
+
+/* One int4 expert: what q4_expert_ptrs() returns, moelan/kernels.py:929-939
+ * (four addresses and the XOR), plus the scale type. */
+typedef struct moe_q4_expert {
+  const void* gu_w; /* gate|up bytes [2I, H/2] */
+  const void* gu_s; /* scales [2I, H/gs] */
+  const void* dn_w; /* down bytes [H, I/2] */
+  const void* dn_s; /* scales [H, I/gs] */
+  uint32_t xor8;    /* 0x88 for stored two's-complement nibbles, 0 for XOR-ed copies */
+  int32_t s_f16;    /* scales are f16 */
+} moe_q4_expert;
+
+/* Bytes of workspace moe_q4_layer needs for P pairs. */
+size_t moe_q4_layer_workspace(int P, int H, int I);
+
+/* out[r] += sum over pairs p of row r of pw[p] * expert(x[r]), for k experts
+ * given as table[eidx[m]] (eidx NULL: table[m]) with pairs poff[m]..poff[m+1]
+ * (input rows prow[p], gate weights pw[p]). Rows touched: rrow[0..nr), whose
+ * pairs are rpair[rptr[i]..rptr[i+1]] in ascending order; each row's sum is
+ * formed in that order and then added to out, as the reference does.
+ * max_rows: the largest poff[m+1]-poff[m]. All arrays: device.
+ * Replaces moe_q4(x, items, H, I, gs, out), moelan/kernels.py:942-968
+ * (_moe_q4 :712-782, float activations). */
+int moe_q4_layer(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k, const int* poff,
+                 const int* prow, const float* pw, int P, const int* rrow, const int* rptr, const int* rpair, int nr,
+                 float* out, int ldo, int H, int I, int gs, int max_rows, void* workspace, size_t ws_bytes,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOEHIP_H */

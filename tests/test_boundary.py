@@ -1,0 +1,87 @@
+"""The C ABI boundary without a GPU: the library loads, exports exactly what
+include/moehip.h declares, the ctypes signatures cover it, and argument
+checks fail loudly with a message (no kernel is launched by these calls)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from distributedmoellm_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "moehip.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(moe_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_is_built_and_loads():
+    assert _lib.LIB_PATH.exists(), "run python -m distributedmoellm_amd.build"
+    assert _lib.load() is not None, _lib.why_not()
+
+
+def test_every_declared_symbol_is_exported():
+    names = header_functions()
+    assert len(names) >= 14
+    L = _lib.lib()
+    for n in names:
+        assert hasattr(L, n), f"{n} is declared in moehip.h but not exported"
+
+
+def test_ctypes_signatures_match_header():
+    assert set(header_functions()) == set(_lib.SIGNATURES)
+
+
+def test_version_and_device_count_without_gpu():
+    L = _lib.lib()
+    assert L.moe_version() == 100
+    assert L.moe_device_count() >= 0
+
+
+def test_struct_layout():
+    assert ctypes.sizeof(_lib.Q4Expert) == 40
+    assert _lib.Q4Expert.xor8.offset == 32
+
+
+@pytest.mark.parametrize("call,needle", [
+    (lambda L: L.moe_q4_matmul_t(1, 1, 1, 1, 0, 8, 96, 7, 0, 1, None), "group size 7"),
+    (lambda L: L.moe_q4_matmul_t(1, 1, 1, 1, 0, 8, 63, 63, 0, 1, None), "even"),
+    (lambda L: L.moe_q4_matmul_t(None, 1, 1, 1, 0, 8, 64, 32, 0, 1, None), "null pointer"),
+    (lambda L: L.moe_q8_matmul_t(1, -1, 1, 1, 0, 8, 64, 32, 1, None), "n=-1"),
+    (lambda L: L.moe_gguf_matmul_t(1, 1, 1, 14, 8, 256, 1, None), "qtype 14"),
+    (lambda L: L.moe_gguf_matmul_t(1, 1, 1, 12, 8, 100, 1, None), "multiple of 256"),
+    (lambda L: L.moe_gguf_dequant(1, 8, 8, 33, 1, None), "multiple of 32"),
+    (lambda L: L.moe_q4_layer(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 32, 1,
+                              1, 10, None), "workspace"),
+    (lambda L: L.moe_q4_layer(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 24, 1,
+                              1, 10, None), "group size 24"),
+    (lambda L: L.moe_combine(1, 8, 1, 1, 1, 1, 1, 1, 8, 16, None), "ldy=8"),
+])
+def test_bad_arguments_fail_with_a_message(call, needle):
+    L = _lib.lib()
+    rc = call(L)
+    assert rc != 0
+    assert needle in _lib.last_error()
+
+
+def test_empty_calls_are_no_ops():
+    L = _lib.lib()
+    assert L.moe_q4_matmul_t(None, 0, None, None, 0, 8, 64, 32, 0, None, None) == 0
+    assert L.moe_q4_layer(None, 64, None, None, 0, None, None, None, 0, None, None, None, 0, None, 64,
+                          64, 32, 32, 0, None, 0, None) == 0
+    assert L.moe_q4_layer_workspace(4, 2048, 768) == 4 * (2 * 768 + 2048) * 4
+
+
+def test_kernels_fail_loudly_without_gpu():
+    from distributedmoellm_amd import kernels
+    import numpy as np
+    if kernels.ENABLED:
+        pytest.skip("a GPU is present")
+    assert kernels.WHY_DISABLED
+    with pytest.raises(RuntimeError, match="not available"):
+        kernels.q4_matmul_t(np.zeros((1, 64), np.float32), np.zeros((8, 32), np.uint8),
+                            np.zeros((8, 2), np.float32), 32, False)

@@ -1,0 +1,137 @@
+"""The fused per-layer int4 call and the store on the GPU, mirroring moelan's
+tests/test_fused.py: the layer call must give what one call per expert gives,
+resident (XOR-ed) and stored copies mix in one call, and everything matches
+the float64 oracle within 1e-5 (norm-wise and per row)."""
+
+import numpy as np
+import pytest
+import torch
+
+from distributedmoellm_amd import experts as X
+from distributedmoellm_amd import gguf as G
+from oracle import restate as R
+
+from test_matvec_gpu import close
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_expert(e):
+    """(Wgu, Wdn, inter) decoded exactly (float64) from an expert's host arrays."""
+    def dec(m):
+        if isinstance(m, X.Packed4):
+            raw = m.raw.cpu().numpy() if isinstance(m.raw, torch.Tensor) else m.raw
+            s = m.s.cpu().numpy() if isinstance(m.s, torch.Tensor) else m.s
+            return R.q4_dequant64(raw, s, m.gs, m.offset)
+        if isinstance(m, X.GroupQuant):
+            return R.q8_dequant64(m.q, m.s, m.gs)
+        if isinstance(m, G.Stacked):
+            return np.concatenate([dec(p) for p in m.parts], 0)
+        if isinstance(m, G.QuantMatrix):
+            return R.gguf_dequant(m.raw, m.qtype, m.shape[1]).astype(np.float64)
+        raise TypeError(m)
+    return dec(e.gu), dec(e.down), e.inter
+
+
+def groups_for(rng, picks):
+    return [(e, np.array(rows), rng.random(len(rows)).astype(np.float32)) for e, rows in picks]
+
+
+@pytest.fixture(scope="module")
+def small_experts():
+    rng = np.random.default_rng(0)
+    return {(1, e): X.synthetic_expert(64, 96, "int4", 32, rng) for e in range(8)}
+
+
+def test_layer_call_matches_one_call_per_expert(kernels, small_experts, monkeypatch):
+    """moelan tests/test_fused.py:37-53 on the device."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    groups = groups_for(rng, [(0, [0]), (2, [0, 3]), (4, [1, 2, 3]), (5, [0, 1, 2, 4, 5]), (7, [5])])
+    got = {}
+    for flag in (False, True):
+        monkeypatch.setattr(kernels, "FUSED", flag)
+        for e in small_experts.values():
+            e.fused = None
+        store = X.ExpertStore(small_experts, fmt="int4")
+        got[flag] = store.compute(1, x, groups)
+    want = R.store_compute(x, groups, lambda e, xr: R.expert_exact(xr, *oracle_expert(small_experts[(1, e)])))
+    close(got[True], want)
+    close(got[False], want)
+    assert np.abs(got[False]).max() > 1e-3
+
+
+def test_layer_call_reads_resident_copies_too(kernels, small_experts):
+    """moelan tests/test_fused.py:57-74: a stored (XOR 0x88) and a resident (offset) expert in one call."""
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    mapped = small_experts[(1, 3)]
+    copy = small_experts[(1, 6)]
+    copy = X.Expert(copy.gu.resident(), copy.down.resident(), copy.inter)
+    assert copy.gu.offset and not mapped.gu.offset
+    w = np.array([0.25, 0.75], np.float32)
+    out = np.zeros_like(x)
+    items = [(kernels.q4_expert_ptrs(mapped), np.array([0, 1]), w),
+             (kernels.q4_expert_ptrs(copy), np.array([1]), w[:1])]
+    kernels.moe_q4(x, items, 64, 96, 32, out)
+    want = np.zeros(x.shape)
+    want[[0, 1]] += R.expert_exact(x[[0, 1]], *oracle_expert(mapped)) * w[:, None]
+    want[[1]] += R.expert_exact(x[[1]], *oracle_expert(copy)) * w[:1, None]
+    close(out, want)
+
+
+def test_layer_call_adds_into_out(kernels, small_experts):
+    """moe_q4 accumulates: out[uniq] += part (moelan/kernels.py:968)."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((4, 64)).astype(np.float32)
+    base = rng.standard_normal((4, 64)).astype(np.float32)
+    e = small_experts[(1, 2)]
+    out = base.copy()
+    kernels.moe_q4(x, [(kernels.q4_expert_ptrs(e), np.array([1, 3]), np.array([0.5, 2.0], np.float32))],
+                   64, 96, 32, out)
+    want = base.astype(np.float64)
+    want[[1, 3]] += R.expert_exact(x[[1, 3]], *oracle_expert(e)) * np.array([[0.5], [2.0]])
+    close(out, want)
+    assert np.array_equal(out[[0, 2]], base[[0, 2]])
+
+
+@pytest.mark.parametrize("rows_per_token,k", [(1, 8), (8, 8), (3, 24)])
+def test_qwen3_30b_layer_decode(kernels, rows_per_token, k):
+    """A layer's picks at the Qwen3-30B-A3B expert shape (H=2048, I=768, gs=32, f16 scales)."""
+    rng = np.random.default_rng(rows_per_token * 10 + k)
+    experts = [X.synthetic_expert(2048, 768, "int4", 32, rng) for _ in range(k)]
+    T = rows_per_token
+    x = rng.standard_normal((T, 2048)).astype(np.float32)
+    items, oitems = [], []
+    for i, e in enumerate(experts):
+        rows = np.sort(rng.choice(T, size=min(T, 1 + i % 3), replace=False)).astype(np.int32)
+        w = rng.random(len(rows)).astype(np.float32)
+        items.append((kernels.q4_expert_ptrs(e), rows, w))
+        oitems.append((lambda xr, e=e: R.expert_exact(xr, *oracle_expert(e)), rows, w))
+    out = np.zeros_like(x)
+    kernels.moe_q4(x, items, 2048, 768, 32, out)
+    close(out, R.moe_q4(x, oitems, np.zeros(x.shape)))
+
+
+def test_expert_call_int4_int8_gguf(kernels):
+    """Expert.__call__ for each format against the oracle's SwiGLU."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 512)).astype(np.float32)
+    for e in (X.synthetic_expert(512, 256, "int4", 32, rng),
+              X.synthetic_expert(512, 256, "int8", 32, rng),
+              G.synthetic_expert(512, 256, ["Q4_K", "Q4_K", "Q8_0"], rng),
+              G.synthetic_expert(512, 256, ["Q8_0", "Q8_0", "Q8_0"], rng)):
+        close(e(x), R.expert_exact(x, *oracle_expert(e)))
+
+
+def test_store_mixes_formats(kernels):
+    rng = np.random.default_rng(4)
+    ex = {(0, 0): X.synthetic_expert(256, 256, "int4", 32, rng),
+          (0, 1): X.synthetic_expert(256, 256, "int8", 32, rng),
+          (0, 2): X.synthetic_expert(256, 256, "int4", 32, rng)}
+    store = X.ExpertStore(ex)
+    x = rng.standard_normal((5, 256)).astype(np.float32)
+    groups = groups_for(rng, [(0, [0, 1, 4]), (1, [1, 2]), (2, [0, 3, 4])])
+    got = store.compute(0, x, groups)
+    want = R.store_compute(x, groups, lambda e, xr: R.expert_exact(xr, *oracle_expert(ex[(0, e)])))
+    close(got, want)

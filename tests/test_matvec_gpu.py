@@ -1,0 +1,196 @@
+"""Decode mat-vec and dequant on the GPU against the oracle, through the C ABI.
+
+Bars: unpacking bit-exact (dequant, one-hot columns); the f32 FMA mat-vec
+within 1e-5 relative to the float64 oracle, norm-wise over the output and per
+output row (tolerance RTOL below). Shapes: the reference test's 96x128, the
+Qwen3-30B-A3B expert (gate|up 1536x2048, down 2048x768), the Qwen3-235B-A22B
+expert (gate|up 3072x4096, down 4096x1536), tiny and odd shapes that take the
+LDS-reduction and generic kernels.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import restate as R
+
+pytestmark = pytest.mark.gpu
+RTOL = 1e-5
+
+
+def close(got, ref, rtol=RTOL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    assert np.all(np.isfinite(got))
+    err = np.linalg.norm(got - ref)
+    assert err <= rtol * np.linalg.norm(ref), f"relative error {err / np.linalg.norm(ref):.3e}"
+    for r in range(ref.shape[0]):
+        e = np.linalg.norm(got[r] - ref[r])
+        assert e <= rtol * max(np.linalg.norm(ref[r]), 1e-30), f"row {r}: {e / np.linalg.norm(ref[r]):.3e}"
+
+
+def int4_matrix(rng, O, I, gs, sdt=np.float16):
+    raw = rng.integers(0, 256, (O, I // 2), dtype=np.uint8)
+    s = (np.abs(rng.normal(0, 0.02, (O, I // gs))) / 8).astype(sdt)
+    return raw, s
+
+
+SHAPES = [(96, 128, 32), (1536, 2048, 32), (2048, 768, 32), (64, 64, 32), (2048, 64, 32), (64, 96, 32),
+          (128, 128, 64), (3072, 4096, 32), (4096, 1536, 32), (40, 8192, 32)]
+
+
+@pytest.mark.parametrize("O,I,gs", SHAPES)
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 17])
+def test_q4_matmul(kernels, O, I, gs, rows):
+    rng = np.random.default_rng(O * 7 + I + rows)
+    raw, s = int4_matrix(rng, O, I, gs)
+    x = rng.standard_normal((rows, I)).astype(np.float32)
+    close(kernels.q4_matmul_t(x, raw, s, gs, False), R.q4_matmul_t(x, raw, s, gs, False))
+
+
+@pytest.mark.parametrize("offset", [False, True])
+@pytest.mark.parametrize("sdt", [np.float16, np.float32])
+def test_q4_offset_and_scale_types(kernels, offset, sdt):
+    rng = np.random.default_rng(1)
+    raw, s = int4_matrix(rng, 1536, 2048, 32, sdt)
+    if sdt == np.float32:
+        s = rng.random(s.shape).astype(np.float32) * 1e-3      # full 24-bit scales
+    x = rng.standard_normal((3, 2048)).astype(np.float32)
+    close(kernels.q4_matmul_t(x, raw, s, 32, offset), R.q4_matmul_t(x, raw, s, 32, offset))
+
+
+@pytest.mark.parametrize("O,I,gs", [(96, 128, 32), (2048, 768, 32), (64, 96, 32)])
+def test_q4_one_hot_columns_are_exact(kernels, O, I, gs):
+    """x = e_c: the kernel returns column c of W bit-exactly (nibble order, sign, scale index)."""
+    rng = np.random.default_rng(2)
+    raw, s = int4_matrix(rng, O, I, gs)
+    W = R.q4_dequant(raw, s, gs, False)
+    cols = [0, 1, 2, 31, 32, 33, I - 2, I - 1]
+    x = np.zeros((len(cols), I), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    y = kernels.q4_matmul_t(x, raw, s, gs, False)
+    for i, c in enumerate(cols):
+        assert np.array_equal(y[i], W[:, c]), f"column {c}"
+
+
+def test_q4_generic_shapes(kernels):
+    """Group sizes that split a 32-column chunk and widths not divisible by 32 take the generic kernel."""
+    rng = np.random.default_rng(3)
+    for O, I, gs in ((24, 64, 16), (10, 48, 16), (7, 20, 10)):
+        raw, s = int4_matrix(rng, O, I, gs, np.float32)
+        x = rng.standard_normal((3, I)).astype(np.float32)
+        close(kernels.q4_matmul_t(x, raw, s, gs, False), R.q4_matmul_t(x, raw, s, gs, False))
+
+
+def test_q4_unaligned_device_buffers(kernels):
+    """Weights at an odd byte offset in HBM: the kernel reads bytes instead of 16-byte words."""
+    rng = np.random.default_rng(4)
+    O, I, gs = 256, 2048, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    big = torch.zeros(raw.size + 1, dtype=torch.uint8, device="cuda")
+    big[1:] = torch.from_numpy(raw.reshape(-1)).cuda()
+    raw_d = big[1:].view(O, I // 2)
+    x = rng.standard_normal((2, I)).astype(np.float32)
+    got = kernels.q4_matmul_t(torch.from_numpy(x).cuda(), raw_d, torch.from_numpy(s).cuda(), gs, False)
+    close(got.cpu().numpy(), R.q4_matmul_t(x, raw, s, gs, False))
+
+
+def test_q4_device_tensors_stay_on_device(kernels):
+    rng = np.random.default_rng(5)
+    raw, s = int4_matrix(rng, 256, 512, 32)
+    x = torch.from_numpy(rng.standard_normal((2, 512)).astype(np.float32)).cuda()
+    y = kernels.q4_matmul_t(x, torch.from_numpy(raw).cuda(), torch.from_numpy(s).cuda(), 32, False)
+    assert isinstance(y, torch.Tensor) and y.is_cuda and y.shape == (2, 256)
+
+
+def test_zero_rows(kernels):
+    raw, s = int4_matrix(np.random.default_rng(0), 64, 64, 32)
+    assert kernels.q4_matmul_t(np.zeros((0, 64), np.float32), raw, s, 32, False).shape == (0, 64)
+
+
+# ---------------------------------------------------------------- int8
+
+@pytest.mark.parametrize("rows", [1, 4, 16, 64])
+@pytest.mark.parametrize("O,I,gs", [(1536, 2048, 32), (2048, 768, 32), (96, 128, 32), (64, 96, 16)])
+def test_q8_matmul(kernels, rows, O, I, gs):
+    rng = np.random.default_rng(rows + O)
+    q = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, (O, I // gs))) / 127).astype(np.float16)
+    x = rng.standard_normal((rows, I)).astype(np.float32)
+    close(kernels.q8_matmul_t(x, q, s, gs), R.q8_matmul_t(x, q, s, gs))
+
+
+def test_q8_one_hot_exact(kernels):
+    rng = np.random.default_rng(6)
+    O, I, gs = 2048, 768, 32
+    q = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    s = rng.random((O, I // gs)).astype(np.float32)
+    W = R.q8_dequant(q, s, gs)
+    cols = [0, 15, 16, 767]
+    x = np.zeros((4, I), np.float32)
+    x[np.arange(4), cols] = 1.0
+    y = kernels.q8_matmul_t(x, q, s, gs)
+    for i, c in enumerate(cols):
+        assert np.array_equal(y[i], W[:, c])
+
+
+# ---------------------------------------------------------------- GGUF
+
+@pytest.mark.parametrize("qtype", [8, 12])
+@pytest.mark.parametrize("rows", [1, 2, 5, 32])
+@pytest.mark.parametrize("O,cols", [(768, 2048), (2048, 768)])
+def test_gguf_matmul(kernels, qtype, rows, O, cols):
+    rng = np.random.default_rng(qtype * 100 + rows + O)
+    raw = R.random_blocks(O, cols, qtype, rng)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    close(kernels.gguf_matmul_t(x, raw, qtype, cols), R.gguf_matmul_t(x, raw, qtype, cols))
+
+
+@pytest.mark.parametrize("qtype", [8, 12])
+def test_gguf_odd_block_counts(kernels, qtype):
+    """Q8_0 rows of an odd number of blocks start 2-byte aligned: the byte path."""
+    rng = np.random.default_rng(7)
+    cols = 32 * 5 if qtype == 8 else 256 * 3
+    raw = R.random_blocks(9, cols, qtype, rng)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    close(kernels.gguf_matmul_t(x, raw, qtype, cols), R.gguf_matmul_t(x, raw, qtype, cols))
+
+
+# ---------------------------------------------------------------- dequant (bit-exact)
+
+@pytest.mark.parametrize("offset", [False, True])
+@pytest.mark.parametrize("sdt", [np.float16, np.float32])
+def test_q4_dequant_bit_exact(kernels, offset, sdt):
+    rng = np.random.default_rng(8)
+    raw, s = int4_matrix(rng, 1536, 2048, 32, sdt)
+    if sdt == np.float32:
+        s = rng.random(s.shape).astype(np.float32)
+    out = np.empty((1536, 2048), np.float32)
+    kernels.q4_dequant(raw, s, 32, offset, out)
+    assert np.array_equal(out, R.q4_dequant(raw, s, 32, offset))
+
+
+def test_q8_dequant_bit_exact(kernels):
+    rng = np.random.default_rng(9)
+    q = rng.integers(-127, 128, (2048, 768), dtype=np.int8)
+    s = rng.random((2048, 24)).astype(np.float32)
+    out = np.empty((2048, 768), np.float32)
+    kernels.q8_dequant(q, s, 32, out)
+    assert np.array_equal(out, R.q8_dequant(q, s, 32))
+
+
+@pytest.mark.parametrize("qtype", [8, 12])
+def test_gguf_dequant_bit_exact_on_random_bytes(kernels, qtype):
+    """Every byte random, Inf/NaN scale fields included (moelan tests/test_gguf.py:25-33 style):
+    finite values equal bit for bit, non-finite ones in the same places."""
+    rng = np.random.default_rng(qtype)
+    cols = 512
+    raw = rng.integers(0, 256, (64, cols // R.QTYPES[qtype][1] * R.QTYPES[qtype][2]), dtype=np.uint8)
+    out = np.empty((64, cols), np.float32)
+    kernels.gguf_dequant(raw, qtype, out)
+    want = R.gguf_dequant(raw, qtype, cols)
+    ok = np.isfinite(want)
+    assert np.array_equal(np.isfinite(out), ok)
+    assert np.array_equal(out[ok], want[ok])
+    assert np.array_equal(np.isnan(out), np.isnan(want))
