@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed-expert path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--stack] [--no-cpu]
+
+Headline (one JSON line on stdout): int4 expert decode mat-vec HBM GB/s.
+A step is one token's 384 routed-expert evaluations at the Qwen3-30B-A3B
+expert shape (48 layers x top-8; H=2048, I=768, int4 group 32, f16 scales) in
+one fused layer call (gate|up, SiLU, down, weighted sum), the experts drawn
+from a resident pool of 1024 (2.7 GB, beyond the 256 MB MALL) so every step
+streams its 1.02 GB of packed weights from HBM. Inputs are resident before the
+timed region. The value is algorithmic bytes (packed nibbles + f16 scales of
+each expert touched once, plus activations) per second over the timed steps.
+
+roofline: the dominant kernel (the int4 decode mat-vec, gate|up and down
+launches) timed with HIP events on the launch stream inside the timed region.
+cpu_baseline: the C/OpenMP restatement of the reference's numba kernel
+(oracle/cpuref.c, _moe_q4 loop structure) on the host cores, a bounded sample.
+
+Extras in the same line: the same 384 evaluations as 48 per-layer calls, the
+Qwen3-235B-A22B-shaped resident stack decode (--stack; 94 layers x 128
+experts, 119 GiB) at B = 1, 8, 32 with Zipf(1.1) routing.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def expert_bytes(H: int, I: int, gs: int, scale_bytes: int = 2) -> int:
+    """Packed nibbles + scales of one expert (gate|up and down)."""
+    n = 3 * H * I
+    return n // 2 + n // gs * scale_bytes
+
+
+class Int4Pool:
+    """n experts of shape (H, I) resident in HBM: one tensor per part, so that
+    expert e's arrays sit at a fixed stride; a device table of moe_q4_expert."""
+
+    def __init__(self, n: int, H: int, I: int, gs: int, seed: int):
+        import torch
+        from distributedmoellm_amd import _lib
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.n, self.H, self.I, self.gs = n, H, I, gs
+        self.gu_w = torch.randint(0, 256, (n, 2 * I, H // 2), dtype=torch.uint8, device="cuda", generator=g)
+        self.dn_w = torch.randint(0, 256, (n, H, I // 2), dtype=torch.uint8, device="cuda", generator=g)
+        # scales |N(0, 0.02)| / 8 in f16
+        self.gu_s = (torch.randn((n, 2 * I, H // gs), device="cuda", generator=g).abs_() * (0.02 / 8)).half()
+        self.dn_s = (torch.randn((n, H, I // gs), device="cuda", generator=g).abs_() * (0.02 / 8)).half()
+        table = (_lib.Q4Expert * n)()
+        for e in range(n):
+            table[e] = _lib.Q4Expert(self.gu_w[e].data_ptr(), self.gu_s[e].data_ptr(), self.dn_w[e].data_ptr(),
+                                     self.dn_s[e].data_ptr(), 0x88, 1)
+        self.table_host = np.frombuffer(bytes(table), np.uint8)
+        self.table = torch.from_numpy(self.table_host.copy()).cuda()
+        torch.cuda.synchronize()
+
+    @property
+    def expert_bytes(self) -> int:
+        return expert_bytes(self.H, self.I, self.gs)
+
+
+class Calls:
+    """Pair lists of a sequence of layer calls, uploaded once (device int32/f32)."""
+
+    def __init__(self, calls):
+        """calls: list of (eidx[k], rows per expert (list of arrays), weights per expert)."""
+        import torch
+        from distributedmoellm_amd import kernels
+        self.items = []
+        parts, spec = [], []
+        for eidx, rows, ws in calls:
+            poff, prow, pw, rrow, rptr, rpair = kernels.pair_lists(rows, ws)
+            spec.append((len(eidx), int(poff[-1]), len(rrow), int(np.diff(poff).max())))
+            parts += [np.asarray(eidx, np.int32).tobytes(), poff.tobytes(), prow.tobytes(), pw.tobytes(),
+                      rrow.tobytes(), rptr.tobytes(), rpair.tobytes()]
+        self.buf, addrs = kernels.upload_parts(parts)
+        for i, (k, P, nr, mr) in enumerate(spec):
+            a = addrs[7 * i:7 * i + 7]
+            self.items.append(dict(eidx=a[0], poff=a[1], prow=a[2], pw=a[3], rrow=a[4], rptr=a[5], rpair=a[6],
+                                   k=k, P=P, nr=nr, max_rows=mr))
+
+
+def run_layer(L, pool, x, out, h, y, c, stream, ev=None):
+    """gate|up mat-vec, down mat-vec (SiLU on load), combine: one layer call."""
+    H, I, gs = pool.H, pool.I, pool.gs
+    tab = pool.table.data_ptr()
+    if ev is not None:
+        ev[0].record()
+    rc = L.moe_q4_experts_matvec(x.data_ptr(), H, c["prow"], tab, c["eidx"], c["k"], c["poff"], 0, H, I, gs,
+                                 c["max_rows"], h.data_ptr(), 2 * I, stream)
+    if ev is not None:
+        ev[1].record()
+    rc |= L.moe_q4_experts_matvec(h.data_ptr(), 2 * I, None, tab, c["eidx"], c["k"], c["poff"], 1, H, I, gs,
+                                  c["max_rows"], y.data_ptr(), H, stream)
+    if ev is not None:
+        ev[2].record()
+    rc |= L.moe_combine(y.data_ptr(), H, c["pw"], c["rrow"], c["rptr"], c["rpair"], c["nr"], out.data_ptr(), H, H,
+                        stream)
+    if rc:
+        from distributedmoellm_amd import _lib
+        raise RuntimeError(_lib.last_error())
+
+
+def decode384(args, L):
+    """One token's 48 x 8 expert evaluations per step, C1 expert shape, from a 1024-expert pool."""
+    import torch
+    H, I, gs, npool, per_step = 2048, 768, 32, 1024, 384
+    log(f"pool: {npool} experts H={H} I={I} gs={gs} ({npool * expert_bytes(H, I, gs) / 1e9:.2f} GB)")
+    pool = Int4Pool(npool, H, I, gs, seed=1)
+    rng = np.random.default_rng(0)
+    nvar = 8
+    fused, per_layer = [], []
+    for v in range(nvar):
+        eidx = np.sort(rng.choice(npool, per_step, replace=False)).astype(np.int32)
+        rows = [np.zeros(1, np.int32) for _ in range(per_step)]
+        ws = [rng.random(1).astype(np.float32) for _ in range(per_step)]
+        fused.append((eidx, rows, ws))
+        for l in range(48):
+            sl = slice(8 * l, 8 * l + 8)
+            per_layer.append((eidx[sl], rows[sl], ws[sl]))
+    cf, cl = Calls(fused), Calls(per_layer)
+    x = torch.randn((1, H), device="cuda")
+    out = torch.zeros((1, H), device="cuda")
+    h = torch.empty((per_step, 2 * I), device="cuda")
+    y = torch.empty((per_step, H), device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    step_bytes = per_step * pool.expert_bytes + 2 * H * 4
+    for i in range(args.warmup):
+        run_layer(L, pool, x, out, h, y, cf.items[i % nvar], stream)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run_layer(L, pool, x, out, h, y, cf.items[i % nvar], stream, evs[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) / args.steps * 1e3
+    gu_ms = np.array([e[0].elapsed_time(e[1]) for e in evs])
+    dn_ms = np.array([e[1].elapsed_time(e[2]) for e in evs])
+    gu_bytes = per_step * (2 * I * H // 2 + 2 * I * (H // gs) * 2) + H * 4
+    dn_bytes = per_step * (H * I // 2 + H * (I // gs) * 2) + per_step * 2 * I * 4
+    # one kernel (the int4 decode mat-vec) serves both launches: average over them
+    avg_s = (gu_ms.mean() + dn_ms.mean()) / 2 / 1e3
+    avg_bytes = (gu_bytes + dn_bytes) / 2
+    res = dict(ms_per_step=ms, value=step_bytes / (ms / 1e3) / 1e9, step_bytes=step_bytes,
+               kernel=dict(name="mv_kernel<FmtQ4, 1, 4> (moe_q4_experts_matvec)", launches=2 * args.steps,
+                           avg_us=avg_s * 1e6, gate_up_us=float(gu_ms.mean() * 1e3),
+                           down_us=float(dn_ms.mean() * 1e3), bytes_per_launch=avg_bytes,
+                           achieved_gbs=avg_bytes / avg_s / 1e9,
+                           gate_up_gbs=gu_bytes / (gu_ms.mean() / 1e3) / 1e9,
+                           down_gbs=dn_bytes / (dn_ms.mean() / 1e3) / 1e9))
+    # the same evaluations as 48 per-layer calls of 8 experts (decode as it runs layer by layer)
+    torch.cuda.synchronize()
+    steps = max(2, args.steps // 2)
+    for i in range(48):
+        run_layer(L, pool, x, out, h, y, cl.items[i], stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        v = s % nvar
+        for l in range(48):
+            run_layer(L, pool, x, out, h, y, cl.items[v * 48 + l], stream)
+    torch.cuda.synchronize()
+    ms_l = (time.perf_counter() - t0) / steps * 1e3
+    res["per_layer_calls"] = dict(ms_per_token=ms_l, gbs=step_bytes / (ms_l / 1e3) / 1e9, calls_per_token=48)
+    res["pool"] = pool
+    return res
+
+
+def cpu_baseline_decode(seconds: float = 12.0):
+    """The reference's fused layer kernel restated in C/OpenMP (oracle/cpuref.c)
+    on the host cores: one token's 384 experts per call from a pool of 64
+    experts (170 MB, beyond the last-level cache), f32 scales as the reference
+    requires; GB/s counted with the same algorithmic bytes as the GPU."""
+    from oracle import build_cpuref
+    L = build_cpuref.load()
+    H, I, gs, npool, per_call = 2048, 768, 32, 64, 384
+    rng = np.random.default_rng(2)
+    gu = [rng.integers(0, 256, (2 * I, H // 2), dtype=np.uint8) for _ in range(npool)]
+    gs_ = [(np.abs(rng.normal(0, 0.02, (2 * I, H // gs))) / 8).astype(np.float16).astype(np.float32)
+           for _ in range(npool)]
+    dn = [rng.integers(0, 256, (H, I // 2), dtype=np.uint8) for _ in range(npool)]
+    ds_ = [(np.abs(rng.normal(0, 0.02, (H, I // gs))) / 8).astype(np.float16).astype(np.float32)
+           for _ in range(npool)]
+    addr = lambda a: a.__array_interface__["data"][0]
+    ptrs = np.array([[addr(gu[e]), addr(gs_[e]), addr(dn[e]), addr(ds_[e])] for e in range(npool)], np.uint64)
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    poff = np.arange(per_call + 1, dtype=np.int64)
+    prow = np.zeros(per_call, np.int64)
+    pw = rng.random(per_call).astype(np.float32)
+    xors = np.full(per_call, 0x88, np.uint8)
+    out = np.zeros((1, H), np.float32)
+
+    def call(i):
+        sel = (np.arange(per_call) + i * 7) % npool
+        pt = np.ascontiguousarray(ptrs[sel].reshape(-1))
+        L.ref_moe_q4(x.ctypes.data, 1, pt.ctypes.data, xors.ctypes.data, poff.ctypes.data, prow.ctypes.data,
+                     pw.ctypes.data, per_call, per_call, H, I, gs, out.ctypes.data)
+    call(0)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        call(n + 1)
+        n += 1
+    dt = time.perf_counter() - t0
+    byts = n * per_call * expert_bytes(H, I, gs)
+    return dict(value=byts / dt / 1e9, unit="GB/s", cores=int(L.ref_threads()), kind="port",
+                sample=f"{n} calls x 384 experts (one token, H=2048 I=768 gs=32) from a 64-expert host pool, "
+                       f"{dt:.1f} s; oracle/cpuref.c ref_moe_q4 (the _moe_q4 loop structure), OpenMP")
+
+
+def zipf_calls(rng, B: int, E: int = 128, k: int = 8, s: float = 1.1):
+    """Top-k per token without replacement from p_r ~ r^-s over a seeded permutation
+    of expert ids; weights softmax(N(0,1)). Returns (eidx, rows per expert, weights)."""
+    perm = rng.permutation(E)
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    picks = {}
+    for t in range(B):
+        ex = perm[rng.choice(E, size=k, replace=False, p=p)]
+        w = np.exp(rng.standard_normal(k))
+        w /= w.sum()
+        for e, wt in zip(ex, w):
+            picks.setdefault(int(e), []).append((t, float(wt)))
+    eidx = np.array(sorted(picks), np.int32)
+    rows = [np.array([t for t, _ in picks[e]], np.int32) for e in eidx]
+    ws = [np.array([w for _, w in picks[e]], np.float32) for e in eidx]
+    return eidx, rows, ws
+
+
+def stack_decode(args, L):
+    """Qwen3-235B-A22B-shaped expert stack resident in HBM, decode steps at B = 1, 8, 32."""
+    import torch
+    H, I, gs, E, layers = 4096, 1536, 32, 128, 94
+    log(f"stack: {layers} layers x {E} experts H={H} I={I} ({layers * E * expert_bytes(H, I, gs) / 2**30:.1f} GiB)")
+    pools = [Int4Pool(E, H, I, gs, seed=100 + l) for l in range(layers)]
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for B in (1, 8, 32):
+        rng = np.random.default_rng(B)
+        nvar = 2
+        calls = Calls([zipf_calls(rng, B) for _ in range(nvar * layers)])
+        dist = np.array([calls.items[i]["k"] for i in range(nvar * layers)]).reshape(nvar, layers)
+        step_bytes = dist.sum(1) * expert_bytes(H, I, gs)
+        Pmax = max(c["P"] for c in calls.items)
+        x = torch.randn((B, H), device="cuda")
+        out = torch.zeros((B, H), device="cuda")
+        h = torch.empty((Pmax, 2 * I), device="cuda")
+        y = torch.empty((Pmax, H), device="cuda")
+
+        def step(v):
+            for l in range(layers):
+                run_layer(L, pools[l], x, out, h, y, calls.items[v * layers + l], stream)
+        for v in range(nvar):
+            step(v)
+        torch.cuda.synchronize()
+        nsteps = max(2, args.steps // 2)
+        t0 = time.perf_counter()
+        for s in range(nsteps):
+            step(s % nvar)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / nsteps * 1e3
+        avg_bytes = float(step_bytes.mean())
+        res[f"B{B}"] = dict(ms_per_step=ms, gbs=avg_bytes / (ms / 1e3) / 1e9, bytes_per_step=avg_bytes,
+                            experts_per_layer=float(dist.mean()),
+                            roofline_ms=avg_bytes / (HBM_PEAK_GBS * 1e9) * 1e3)
+        log(f"stack B={B}: {ms:.3f} ms/step, {res[f'B{B}']['gbs']:.0f} GB/s, {dist.mean():.1f} experts/layer")
+    del pools
+    torch.cuda.empty_cache()
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this path's kernels run on one MI355X and --gpus {args.gpus} "
+              f"is not supported (sharding is described in DESIGN.md).", file=sys.stderr)
+        return 2
+    import torch
+    from distributedmoellm_amd import _lib, kernels
+    if not kernels.ENABLED:
+        raise SystemExit(f"HIP kernels unavailable: {kernels.WHY_DISABLED}")
+    L = _lib.lib()
+    info = _lib.device_info(torch.cuda.current_device())
+    log(f"device {info}")
+
+    r = decode384(args, L)
+    log(f"decode384: {r['ms_per_step']:.3f} ms/step, {r['value']:.0f} GB/s; kernel {r['kernel']['achieved_gbs']:.0f} GB/s")
+    del r["pool"]
+    torch.cuda.empty_cache()
+    extras = {"per_layer_calls": r.pop("per_layer_calls")}
+    if args.stack:
+        extras["stack_235b"] = stack_decode(args, L)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline_decode()
+        log(f"cpu baseline: {cpu['value']:.1f} GB/s on {cpu['cores']} threads")
+    k = r["kernel"]
+    line = {
+        "metric": "int4 expert mat-vec HBM GB/s (% peak); MoE-layer prefill tokens/sec on 1 GPU",
+        "value": round(r["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4xf32",
+        "data": "synthetic (seeded uniform nibbles, |N(0,0.02)|/8 f16 scales, N(0,1) activations)",
+        "config": {"workload": "int4 expert decode mat-vec: one token's 384 routed-expert evaluations "
+                               "(48 layers x top-8) per fused call, Qwen3-30B-A3B expert shape H=2048 I=768, "
+                               "int4 group 32, f16 scales, from a 1024-expert HBM pool (2.7 GB)",
+                   "experts_per_step": 384, "rows_per_expert": 1, "bytes_per_step": r["step_bytes"]},
+        "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(k["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(k["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": k["name"], "avg_launch_us": round(k["avg_us"], 2),
+                     "bytes_per_launch": k["bytes_per_launch"],
+                     "gate_up": {"us": round(k["gate_up_us"], 2), "gbs": round(k["gate_up_gbs"], 1)},
+                     "down": {"us": round(k["down_us"], 2), "gbs": round(k["down_gbs"], 1)}},
+        "cpu_baseline": cpu,
+        "extras": extras,
+        "device": info,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -47,6 +47,7 @@ SIGNATURES = {
     "moe_gguf_dequant": (c_int, [_P, _I, _I, _I, _P, _P]),
     "moe_silu_mul": (c_int, [_P, _I, _I, _I, _P, _I, _P]),
     "moe_combine": (c_int, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    "moe_q4_experts_matvec": (c_int, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
     "moe_q4_layer_workspace": (c_size_t, [_I, _I, _I]),
     "moe_q4_layer": (c_int, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I,
                              _I, _I, _I, _I, _P, _Z, _P]),

@@ -231,3 +231,32 @@ MOE_API int moe_combine(const float* y, int ldy, const float* pw, const int* rro
   REQUIRE(y && pw && rrow && rptr && rpair && out, "moe_combine: null pointer");
   return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, as_stream(stream));
 }
+
+MOE_API int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4_expert* table,
+                                  const int* eidx, int k, const int* poff, int which, int H, int I, int gs,
+                                  int max_rows, float* y, int ldy, void* stream) {
+  REQUIRE(which == 0 || which == 1, "moe_q4_experts_matvec: which=%d (0 gate|up, 1 down)", which);
+  REQUIRE(H > 0 && I > 0 && H % 2 == 0 && I % 2 == 0, "moe_q4_experts_matvec: H=%d and I=%d must be positive and even",
+          H, I);
+  REQUIRE(gs > 0 && gs % 2 == 0 && H % gs == 0 && I % gs == 0,
+          "moe_q4_experts_matvec: group size %d must divide H=%d and I=%d", gs, H, I);
+  REQUIRE(k >= 0 && max_rows >= 0, "moe_q4_experts_matvec: k=%d max_rows=%d", k, max_rows);
+  if (k == 0 || max_rows == 0) return MOE_OK;
+  REQUIRE(x && table && poff && y, "moe_q4_experts_matvec: null pointer");
+  const int O = which ? H : 2 * I, cols = which ? I : H;
+  REQUIRE(ldx >= (which ? 2 * I : H) && ldy >= O, "moe_q4_experts_matvec: ldx=%d ldy=%d too small", ldx, ldy);
+  MVShape sh;
+  plan_matvec(FMT_Q4, O, cols, gs, &sh);
+  MVJob j{};
+  j.x = x;
+  j.ldx = ldx;
+  j.y = y;
+  j.ldy = ldy;
+  j.seg = poff;
+  j.xrow = xrow;
+  j.experts = reinterpret_cast<const ExpertDesc*>(table);
+  j.eidx = eidx;
+  j.which = which;
+  j.half_in = which ? I : 0;
+  return run_matvec(FMT_Q4, sh, j, k, max_rows, as_stream(stream));
+}

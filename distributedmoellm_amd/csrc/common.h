@@ -29,9 +29,18 @@ __host__ __device__ inline bool aligned(const void* p, size_t a) { return (reint
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// 16 bytes that are read once: a non-temporal 128-bit load
+// Pointers in the global address space: loads through them are global_load_*
+// (counted by vmcnt only), not flat loads, even when the address came from memory.
+#define MOE_GLOBAL __attribute__((address_space(1)))
+
+template <class T>
+__device__ __forceinline__ const MOE_GLOBAL T* gptr(const void* p) {
+  return (const MOE_GLOBAL T*)(uintptr_t)p;
+}
+
+// 16 bytes that are read once: a non-temporal 128-bit global load
 __device__ __forceinline__ uint4 stream_load16(const void* p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 v = __builtin_nontemporal_load(gptr<u32x4>(p));
   return uint4{v.x, v.y, v.z, v.w};
 }
 

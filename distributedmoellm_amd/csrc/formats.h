@@ -19,14 +19,56 @@ namespace moe {
 
 // Where the activations of one input row come from: a plain f32 row, or the
 // gate|up output h of an expert (2*I values) turned into silu(gate) * up.
+// A chunk's activations are runs of consecutive columns, read with 16-byte
+// loads when the row allows it; the silu/plain choice is made once per run.
 struct XSrc {
   const float* row;
   int half;  // > 0: silu input, h[c] is gate, h[half + c] is up
+  bool a16;  // row (and, for silu, row + half) 16-byte aligned
+
+  template <int N>
+  __device__ __forceinline__ void raw(const float* p, float* v) const {
+    if (a16) {
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) {
+        const float4 q = reinterpret_cast<const float4*>(p)[i];
+        v[4 * i] = q.x;
+        v[4 * i + 1] = q.y;
+        v[4 * i + 2] = q.z;
+        v[4 * i + 3] = q.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[i] = p[i];
+    }
+  }
+
+  // v[0..N) = activations of columns c0 .. c0+N-1 (N a multiple of 4, c0 of 4)
+  template <int N>
+  __device__ __forceinline__ void run(int c0, float* v) const {
+    if (half > 0) {
+      float u[N];
+      raw<N>(row + c0, v);
+      raw<N>(row + half + c0, u);
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[i] = silu(v[i]) * u[i];
+    } else {
+      raw<N>(row + c0, v);
+    }
+  }
+
+  // one column (generic kernels)
   __device__ __forceinline__ float operator()(int c) const {
     if (half > 0) return silu(row[c]) * row[half + c];
     return row[c];
   }
 };
+
+__device__ __forceinline__ XSrc make_xsrc(const float* x, int ldx, int xrow, int half) {
+  const float* row = x + (size_t)xrow * ldx;
+  const bool a = aligned(row, 16) && (half % 4) == 0;
+  return XSrc{row, half, a};
+}
 
 // ------------------------------------------------------------------ Q4
 struct FmtQ4 {
@@ -40,11 +82,12 @@ struct FmtQ4 {
   //   lo*x[2m] + hi*x[2m+1] = lo*xr[m] + b*xr[16+m]
   // so one masked word and the raw word feed v_cvt_f32_ubyteK directly.
   __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
-    const int c0 = chunk * 32;
+    float v[32];
+    xs.run<32>(chunk * 32, v);
     float sum = 0.f;
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
-      const float xe = xs(c0 + 2 * m), xo = xs(c0 + 2 * m + 1);
+      const float xe = v[2 * m], xo = v[2 * m + 1];
       xr[m] = xe - xo * 0.0625f;
       xr[16 + m] = xo * 0.0625f;
       sum += xe + xo;
@@ -76,10 +119,7 @@ struct FmtQ8 {
   static constexpr int BYTES = 16;
   static constexpr bool GGUF = false;
 
-  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) xr[j] = xs(chunk * 16 + j);
-  }
+  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) { xs.run<16>(chunk * 16, xr); }
 
   __device__ static float dot(const uint4 w, uint32_t, const float* xr) {
     const uint32_t a[4] = {w.x, w.y, w.z, w.w};
@@ -99,10 +139,7 @@ struct FmtQ8_0 {
   static constexpr int BYTES = 34;
   static constexpr bool GGUF = true;
 
-  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
-#pragma unroll
-    for (int j = 0; j < 32; ++j) xr[j] = xs(chunk * 32 + j);
-  }
+  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) { xs.run<32>(chunk * 32, xr); }
 
   // One block at byte offset 34*chunk. With a 4-byte aligned row start only
   // aligned dword (and one ushort) loads are used, realigned with v_alignbyte;
@@ -153,11 +190,11 @@ struct FmtQ4K {
 
   __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
     const int c0 = col_lo(chunk);
+    xs.run<16>(c0, xr);
+    xs.run<16>(c0 + 32, xr + 16);
     float slo = 0.f, shi = 0.f;
 #pragma unroll
     for (int l = 0; l < 16; ++l) {
-      xr[l] = xs(c0 + l);
-      xr[16 + l] = xs(c0 + 32 + l);
       slo += xr[l];
       shi += xr[16 + l];
     }

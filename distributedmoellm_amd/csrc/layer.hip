@@ -10,29 +10,64 @@
 
 namespace moe {
 
-// part = sum over the row's pairs, in order, of w * y; then out[row] += part.
-__global__ void combine_kernel(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr,
-                               const int* rpair, float* out, int ldo, int H) {
+// part = sum over the row's pairs of w * y; then out[row] += part. A block
+// takes one touched row and 256 columns (64 threads x 4 columns); its 4 waves
+// sum interleaved quarters of the row's pair list, which are then added in a
+// fixed order: deterministic, and no atomics.
+__global__ __launch_bounds__(256) void combine_kernel(const float* y, int ldy, const float* pw, const int* rrow,
+                                                      const int* rptr, const int* rpair, float* out, int ldo, int H,
+                                                      int vec4) {
+  __shared__ float4 part[4][64];
   const int i = blockIdx.y;
   const int q0 = rptr[i], q1 = rptr[i + 1];
-  float* dst = out + (size_t)rrow[i] * ldo;
-  for (int o = blockIdx.x * blockDim.x + threadIdx.x; o < H; o += gridDim.x * blockDim.x) {
-    float part = 0.f;
-    for (int q = q0; q < q1; ++q) {
+  const int seg = threadIdx.x >> 6, t = threadIdx.x & 63;
+  const int c = blockIdx.x * 256 + 4 * t;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < H) {
+    for (int q = q0 + seg; q < q1; q += 4) {
       const int p = rpair[q];
-      part += pw[p] * y[(size_t)p * ldy + o];
+      const float w = pw[p];
+      const float* yp = y + (size_t)p * ldy + c;
+      if (vec4) {
+        const float4 v = *reinterpret_cast<const float4*>(yp);
+        a.x += w * v.x;
+        a.y += w * v.y;
+        a.z += w * v.z;
+        a.w += w * v.w;
+      } else {
+        a.x += w * yp[0];
+        if (c + 1 < H) a.y += w * yp[1];
+        if (c + 2 < H) a.z += w * yp[2];
+        if (c + 3 < H) a.w += w * yp[3];
+      }
     }
-    dst[o] += part;
+  }
+  part[seg][t] = a;
+  __syncthreads();
+  if (seg == 0 && c < H) {
+    float4 s = part[0][t];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      const float4 v = part[k][t];
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    float* dst = out + (size_t)rrow[i] * ldo + c;
+    dst[0] += s.x;
+    if (c + 1 < H) dst[1] += s.y;
+    if (c + 2 < H) dst[2] += s.z;
+    if (c + 3 < H) dst[3] += s.w;
   }
 }
 
 int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
                 float* out, int ldo, int H, hipStream_t st) {
   if (nr <= 0) return MOE_OK;
-  const int threads = 256;
-  int gx = (H + threads - 1) / threads;
-  if (gx > 64) gx = 64;
-  hipLaunchKernelGGL(combine_kernel, dim3(gx, nr), dim3(threads), 0, st, y, ldy, pw, rrow, rptr, rpair, out, ldo, H);
+  const int vec4 = (H % 4 == 0 && ldy % 4 == 0 && aligned(y, 16)) ? 1 : 0;
+  hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, nr), dim3(256), 0, st, y, ldy, pw, rrow, rptr, rpair, out,
+                     ldo, H, vec4);
   return check_launch("weighted combine");
 }
 

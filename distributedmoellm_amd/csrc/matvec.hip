@@ -19,6 +19,10 @@
 #include "formats.h"
 #include "matvec.h"
 
+#include <stdlib.h>
+
+#include <type_traits>
+
 namespace moe {
 
 // 16 weight bytes of a row: one 128-bit load when the matrix is 16-byte
@@ -103,7 +107,7 @@ __global__ __launch_bounds__(256) void mv_kernel(MVShape sh, MVJob job) {
       if (lane_on && pb + r < p1) {
         const int p = pb + r;
         const int xrow = job.xrow ? job.xrow[p] : p;
-        XSrc xs{job.x + (size_t)xrow * job.ldx, job.half_in};
+        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
         F::load_x(xs, c, xr[r]);
       } else {
 #pragma unroll
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(256) void mv_gguf_kernel(MVShape sh, MVJob job) {
       if (lane_on && pb + r < p1) {
         const int p = pb + r;
         const int xrow = job.xrow ? job.xrow[p] : p;
-        XSrc xs{job.x + (size_t)xrow * job.ldx, job.half_in};
+        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
         F::load_x(xs, c, xr[r]);
       } else {
 #pragma unroll
@@ -200,6 +204,178 @@ __global__ __launch_bounds__(256) void mv_gguf_kernel(MVShape sh, MVJob job) {
   }
 }
 
+// ------------------------------------------------------------------ streaming kernel
+//
+// The decode kernel for rows whose chunk count is a multiple of 8 (every
+// expert shape of interest): L lanes per row (8, 16, 32 or 64), CPL chunks per
+// lane, so a wave covers 64/L rows per pass. Each wave owns a run of ng groups
+// of G passes; its activations are prepared once into registers, weight loads
+// for group g+1 are issued before group g is computed (two register buffers),
+// and a row's partial sums are added across its L lanes with DPP row shifts /
+// broadcasts (v_add_f32_dpp: no LDS, no barrier). Waves of a block are
+// independent.
+
+template <int CTRL, int ROWMASK, bool BC>
+__device__ __forceinline__ float dpp_read(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, BC));
+}
+
+// lane L-1 of every aligned group of L lanes receives the group's sum
+__device__ __forceinline__ float lane_group_sum(float v, int L) {
+  v += dpp_read<0x111, 0xf, true>(v);  // row_shr:1
+  v += dpp_read<0x112, 0xf, true>(v);  // row_shr:2
+  v += dpp_read<0x114, 0xf, true>(v);  // row_shr:4
+  if (L >= 16) v += dpp_read<0x118, 0xf, true>(v);   // row_shr:8
+  if (L >= 32) v += dpp_read<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1, 3
+  if (L >= 64) v += dpp_read<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// passes per register buffer, by chunks per lane and input rows
+template <int CPL, int NR>
+constexpr int fast_group() {
+  return (CPL * NR >= 6) ? 1 : (CPL * NR >= 2 ? 2 : 4);
+}
+
+// 16 weight bytes with the alignment known at compile time
+template <bool A16>
+__device__ __forceinline__ uint4 wload16(const uint8_t* p) {
+  if constexpr (A16) {
+    return stream_load16(p);
+  } else {
+    const MOE_GLOBAL uint8_t* q = gptr<uint8_t>(p);
+    uint32_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = q[4 * i] | (q[4 * i + 1] << 8) | (q[4 * i + 2] << 16) | ((uint32_t)q[4 * i + 3] << 24);
+    return uint4{v[0], v[1], v[2], v[3]};
+  }
+}
+
+template <bool SF16>
+__device__ __forceinline__ float sload(const void* s, size_t idx) {
+  if constexpr (SF16) return half_bits_to_float(gptr<uint16_t>(s)[idx]);
+  else return gptr<float>(s)[idx];
+}
+
+template <class F, int CPL, int NR, bool SF16, bool A16>
+__device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job, const MatRef& M, int L, int A,
+                                             int ng, int p0, int p1, int row_begin) {
+  constexpr int G = fast_group<CPL, NR>();
+  const int lane = threadIdx.x & 63;
+  const int rpp = 64 / L, lg = lane / L, lc = lane % L;
+  const bool active = lc < A;  // the first A lanes of a group own the row's chunks
+  const int gdiv = sh.gs / F::VALS;  // chunks per scale group (gs is a multiple of VALS here)
+
+  for (int pb = p0; pb < p1; pb += NR) {
+    float xr[NR][CPL][F::XR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (pb + r < p1) {
+        const int p = pb + r;
+        const int xrow = job.xrow ? job.xrow[p] : p;
+        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          if (active) F::load_x(xs, lc + c * A, xr[r][c]);
+          else
+#pragma unroll
+            for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+      }
+    }
+
+    uint4 wb[2][G][CPL];
+    float sb[2][G][CPL];
+    // buffers are named by compile-time constants only, so they stay in VGPRs
+    auto issue = [&](auto buf, int grp) {
+      constexpr int B = decltype(buf)::value;
+      const int rbase = row_begin + grp * G * rpp + lg;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int o = rbase + g * rpp;
+        const bool on = o < sh.O && grp < ng && active;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const int chunk = lc + c * A;
+          // rows past the end read row 0 (in bounds) and are dropped below
+          const int oo = on ? o : 0;
+          const int cc = on ? chunk : 0;
+          // unconditional loads (always in bounds): no branch, so no wait between them
+          wb[B][g][c] = wload16<A16>(M.w + (size_t)oo * sh.row_bytes + (size_t)cc * 16);
+          const float sv = sload<SF16>(M.s, (size_t)oo * sh.G + cc / gdiv);
+          sb[B][g][c] = on ? sv : 0.f;
+        }
+      }
+    };
+    auto compute = [&](auto buf, int grp) {
+      constexpr int B = decltype(buf)::value;
+      const int rbase = row_begin + grp * G * rpp + lg;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float a = 0.f;
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) a = fmaf(F::dot(wb[B][g][c], M.xor4, xr[r][c]), sb[B][g][c], a);
+          acc[r] = lane_group_sum(a, L);
+        }
+        const int o = rbase + g * rpp;
+        if (lc == L - 1 && o < sh.O) {
+#pragma unroll
+          for (int r = 0; r < NR; ++r)
+            if (pb + r < p1) job.y[(size_t)(pb + r) * job.ldy + o] = acc[r];
+        }
+      }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    issue(B0{}, 0);
+    for (int grp = 0; grp < ng; grp += 2) {
+      issue(B1{}, grp + 1);
+      compute(B0{}, grp);
+      if (grp + 1 < ng) {
+        issue(B0{}, grp + 2);
+        compute(B1{}, grp + 1);
+      }
+    }
+  }
+}
+
+// One launch covers every matrix of the call (grid.y); the scale type and the
+// weight alignment are uniform per matrix, so the specialised body is chosen
+// once at the top.
+template <class F, int CPL, int NR>
+__global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int L, int A, int ng) {
+  constexpr int G = fast_group<CPL, NR>();
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  if (p0 >= p1) return;
+  const int wave = threadIdx.x >> 6;
+  const int wave_rows = ng * G * (64 / L);
+  const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * wave_rows;
+  if (row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
+  const MatRef M = resolve(job, mat);
+  const bool a16 = aligned(M.w, 16);
+  if (M.s_f16) {
+    if (a16) mv_fast_body<F, CPL, NR, true, true>(sh, job, M, L, A, ng, p0, p1, row_begin);
+    else mv_fast_body<F, CPL, NR, true, false>(sh, job, M, L, A, ng, p0, p1, row_begin);
+  } else {
+    if (a16) mv_fast_body<F, CPL, NR, false, true>(sh, job, M, L, A, ng, p0, p1, row_begin);
+    else mv_fast_body<F, CPL, NR, false, false>(sh, job, M, L, A, ng, p0, p1, row_begin);
+  }
+}
+
 // Any shape the chunked kernels do not take (group sizes that split a chunk,
 // unaligned rows): one thread per (output row, input row), straight loops.
 __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
@@ -214,7 +390,7 @@ __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < (long)np * sh.O; i += (long)gridDim.x * blockDim.x) {
     const int p = p0 + (int)(i / sh.O), o = (int)(i % sh.O);
     const int xrow = job.xrow ? job.xrow[p] : p;
-    XSrc xs{job.x + (size_t)xrow * job.ldx, job.half_in};
+    const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
     const uint8_t* row = M.w + (size_t)o * sh.row_bytes;
     float acc = 0.f;
     if (fmt == FMT_Q4) {
@@ -300,8 +476,8 @@ int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh) {
   sh->G = (fmt == FMT_Q4 || fmt == FMT_Q8) ? I / gs : 0;
   sh->row_bytes = bytes_per_row(fmt, I);
   const int v = vals_per_chunk(fmt);
-  sh->cpr = I / v;
-  sh->rpp = sh->cpr >= 256 ? 1 : 256 / sh->cpr;
+  sh->cpr = I / v;  // 0 when a row is narrower than one chunk: generic kernel
+  sh->rpp = sh->cpr >= 256 || sh->cpr < 1 ? 1 : 256 / sh->cpr;
   sh->pow2 = (sh->cpr <= 64 && (sh->cpr & (sh->cpr - 1)) == 0) ? 1 : 0;
   return MOE_OK;
 }
@@ -337,9 +513,72 @@ static void launch_fmt(const MVShape& sh, const MVJob& job, int nmat, int max_ro
   else launch_nr<F, 4, P>(sh, job, nmat, st);
 }
 
+template <class F, int CPL>
+static void launch_fast_cpl(const MVShape& sh, const MVJob& job, int nmat, int nr, int L, int A, hipStream_t st) {
+  auto go = [&](auto kernel, int G) {
+    const int rpp = 64 / L;
+    const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));  // wave groups in the launch
+    // runs of several groups per wave amortise the activation set-up; keep
+    // at least ~8 waves per CU of the 256 in flight
+    int ng = (int)(groups / 2048);
+    ng = ng < 1 ? 1 : (ng > 8 ? 8 : ng);
+    const int wave_rows = ng * G * rpp;
+    const int waves = (sh.O + wave_rows - 1) / wave_rows;
+    dim3 grid((waves + 3) / 4, nmat);
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, sh, job, L, A, ng);
+  };
+  if (nr == 1) go(mv_fast_kernel<F, CPL, 1>, fast_group<CPL, 1>());
+  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, CPL, 2>, fast_group<CPL, 2>());
+  else go(mv_fast_kernel<F, 1, 4>, fast_group<1, 4>());
+}
+
+// Lanes per row: by default one chunk per lane whenever a row has at most 64
+// chunks (idle lanes fill a power-of-two group if it stays >= 3/4 busy),
+// otherwise power-of-two groups with several chunks per lane. MOEHIP_MV_DENSE=1
+// always takes the latter (for measurements).
+static void lanes_for(int cpr, int* L, int* A, int* cpl) {
+  static const int dense = [] {
+    const char* e = getenv("MOEHIP_MV_DENSE");
+    return e && e[0] == '1';
+  }();
+  if (!dense && cpr <= 64) {
+    int l = 8;
+    while (l < cpr) l <<= 1;
+    if (4 * cpr >= 3 * l) {
+      *L = l;
+      *A = cpr;
+      *cpl = 1;
+      return;
+    }
+  }
+  int l = 64;
+  while (cpr % l) l >>= 1;
+  *L = l;
+  *A = l;
+  *cpl = cpr / l;
+}
+
+template <class F>
+static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
+  if (sh.cpr % 8 != 0) return false;
+  int L, A, cpl;
+  lanes_for(sh.cpr, &L, &A, &cpl);
+  if (L < 8 || cpl > 4) return false;
+  const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
+  switch (cpl) {
+    case 1: launch_fast_cpl<F, 1>(sh, job, nmat, nr, L, A, st); return true;
+    case 2: launch_fast_cpl<F, 2>(sh, job, nmat, nr, L, A, st); return true;
+    case 3: launch_fast_cpl<F, 3>(sh, job, nmat, nr, L, A, st); return true;
+    case 4: launch_fast_cpl<F, 4>(sh, job, nmat, nr, L, A, st); return true;
+  }
+  return false;
+}
+
 int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   if (max_rows <= 0 || nmat <= 0 || sh.O <= 0) return MOE_OK;
   if (chunked_ok(fmt, sh)) {
+    if (fmt == FMT_Q4 && launch_fast<FmtQ4>(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec");
+    if (fmt == FMT_Q8 && launch_fast<FmtQ8>(sh, job, nmat, max_rows, st)) return check_launch("int8 mat-vec");
     const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
     const size_t lds = sh.pow2 ? 0 : (size_t)4 * nr * sh.rpp * (sh.cpr + 1) * sizeof(float);
     if (lds <= 64 * 1024) {

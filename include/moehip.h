@@ -128,6 +128,16 @@ int moe_q4_layer(const float* x, int ldx, const moe_q4_expert* table, const int*
                  float* out, int ldo, int H, int I, int gs, int max_rows, void* workspace, size_t ws_bytes,
                  void* stream);
 
+/* One sweep of the layer call over its experts' matrices: for expert
+ * table[eidx[m]] (eidx NULL: table[m]) and its pairs p in poff[m]..poff[m+1],
+ * y[p] = xin(p) @ W.T where W is the gate|up matrix (which = 0; xin(p) = x row
+ * xrow[p], or row p when xrow is NULL) or the down matrix (which = 1; xin(p)
+ * = silu(h[:, :I]) * h[:, I:] of row p of x = h, the gate|up outputs).
+ * The gate|up and down phases of _moe_q4, moelan/kernels.py:727-745, 749-777. */
+int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4_expert* table, const int* eidx,
+                          int k, const int* poff, int which, int H, int I, int gs, int max_rows, float* y, int ldy,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif
