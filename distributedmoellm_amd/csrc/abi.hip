@@ -9,6 +9,7 @@
 #include "dequant.h"
 #include "layer.h"
 #include "matvec.h"
+#include "prefill.h"
 
 static_assert(sizeof(moe_q4_expert) == sizeof(moe::ExpertDesc), "moe_q4_expert layout");
 static_assert(offsetof(moe_q4_expert, xor8) == offsetof(moe::ExpertDesc, xor8), "moe_q4_expert layout");
@@ -259,4 +260,218 @@ MOE_API int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, cons
   j.which = which;
   j.half_in = which ? I : 0;
   return run_matvec(FMT_Q4, sh, j, k, max_rows, as_stream(stream));
+}
+
+// ------------------------------------------------------------------ prefill
+
+namespace moe {
+static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// largest token count one grouping workgroup takes (its bitsets live in LDS)
+static int max_group_tokens(int E) {
+  const size_t lds = 56 * 1024;  // of 64 KB: the kernel's own counters take the rest
+  const size_t words = lds / (2 * sizeof(uint32_t) * (size_t)E);
+  return (int)(words * 32);
+}
+
+struct PrefillWs {
+  float* logits;
+  int* idx;
+  float* w;
+  int* eoff;
+  int* rows;
+  float* wts;
+  int* pos;
+  int* experts;
+  int* offsets;
+  int* n_used;
+  _Float16* xs;
+  _Float16* act;
+  float* y;
+  size_t bytes;
+};
+
+static PrefillWs prefill_layout(void* base, int T, int E, int k, int H, int I) {
+  PrefillWs w{};
+  const size_t P = (size_t)T * k;
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off += align256(n);
+    return (char*)base + o;
+  };
+  w.logits = (float*)take((size_t)T * E * 4);
+  w.idx = (int*)take(P * 4);
+  w.w = (float*)take(P * 4);
+  w.eoff = (int*)take(((size_t)E + 1) * 4);
+  w.rows = (int*)take(P * 4);
+  w.wts = (float*)take(P * 4);
+  w.pos = (int*)take(P * 4);
+  w.experts = (int*)take((size_t)E * 4);
+  w.offsets = (int*)take(((size_t)E + 1) * 4);
+  w.n_used = (int*)take(4);
+  w.xs = (_Float16*)take(P * H * 2);
+  w.act = (_Float16*)take(P * I * 2);
+  w.y = (float*)take(P * H * 4);
+  w.bytes = off;
+  return w;
+}
+
+static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nexp, const int* eoff, const int* rows,
+                       int P, int H, int I, int gs, _Float16* xs, _Float16* act, float* y, int ldy, hipStream_t st) {
+  int rc = run_gather_f16(x, ldx, rows, P, H, xs, st);
+  if (rc) return rc;
+  GemmArgs g{};
+  g.A = xs;
+  g.lda = H;
+  g.eoff = eoff;
+  g.table = table;
+  g.which = 0;
+  g.K = H;
+  g.I = I;
+  g.gs = gs;
+  g.act = act;
+  g.ldact = I;
+  rc = run_gemm(MODE_GATE_UP, g, nexp, st);
+  if (rc) return rc;
+  GemmArgs d{};
+  d.A = act;
+  d.lda = I;
+  d.eoff = eoff;
+  d.table = table;
+  d.which = 1;
+  d.K = I;
+  d.N = H;
+  d.gs = gs;
+  d.Y = y;
+  d.ldy = ldy;
+  return run_gemm(MODE_DOWN, d, nexp, st);
+}
+
+static int check_mfma_shape(const char* who, int H, int I, int gs) {
+  REQUIRE(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0, "%s: H=%d and I=%d must be multiples of 128", who, H, I);
+  REQUIRE(gs > 0 && gs % 32 == 0 && H % gs == 0 && I % gs == 0,
+          "%s: group size %d must be a multiple of 32 dividing H=%d and I=%d", who, gs, H, I);
+  return MOE_OK;
+}
+}  // namespace moe
+
+MOE_API int moe_router_logits(const float* x, int ldx, const float* router, int T, int E, int H, float* logits,
+                              void* stream) {
+  REQUIRE(T >= 0 && E > 0 && H > 0 && ldx >= H, "moe_router_logits: T=%d E=%d H=%d ldx=%d", T, E, H, ldx);
+  if (T == 0) return MOE_OK;
+  REQUIRE(x && router && logits, "moe_router_logits: null pointer");
+  return run_router_logits(x, ldx, router, T, E, H, logits, as_stream(stream));
+}
+
+MOE_API int moe_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, void* stream) {
+  REQUIRE(E > 0 && E <= 256, "moe_route: E=%d (1..256 experts)", E);
+  REQUIRE(k > 0 && k <= E && k <= 64, "moe_route: k=%d for E=%d", k, E);
+  REQUIRE(T >= 0, "moe_route: T=%d", T);
+  if (T == 0) return MOE_OK;
+  REQUIRE(logits && idx && w, "moe_route: null pointer");
+  return run_route(logits, T, E, k, normalize, idx, w, as_stream(stream));
+}
+
+MOE_API int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts,
+                                int* pos, int* experts, int* offsets, int* n_used, void* stream) {
+  REQUIRE(E > 0 && E <= 1024 && k > 0 && T >= 0, "moe_group_by_expert: T=%d k=%d E=%d", T, k, E);
+  REQUIRE(T <= max_group_tokens(E), "moe_group_by_expert: %d tokens exceed one pass (%d for %d experts)", T,
+          max_group_tokens(E), E);
+  REQUIRE(idx && w && eoff && rows && wts && pos && experts && offsets && n_used, "moe_group_by_expert: null pointer");
+  return run_group(idx, w, T, k, E, eoff, rows, wts, pos, experts, offsets, n_used, as_stream(stream));
+}
+
+MOE_API size_t moe_q4_grouped_ffn_workspace(int P, int H, int I) {
+  if (P <= 0 || H <= 0 || I <= 0) return 0;
+  return align256((size_t)P * H * 2) + align256((size_t)P * I * 2);
+}
+
+MOE_API int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* table, int nexp, const int* eoff,
+                               const int* rows, int P, int H, int I, int gs, float* y, int ldy, void* workspace,
+                               size_t ws_bytes, void* stream) {
+  if (int rc = check_mfma_shape("moe_q4_grouped_ffn", H, I, gs)) return rc;
+  REQUIRE(nexp >= 0 && P >= 0 && ldx >= H && ldy >= H, "moe_q4_grouped_ffn: nexp=%d P=%d ldx=%d ldy=%d", nexp, P, ldx,
+          ldy);
+  if (nexp == 0 || P == 0) return MOE_OK;
+  REQUIRE(x && table && eoff && rows && y, "moe_q4_grouped_ffn: null pointer");
+  const size_t need = moe_q4_grouped_ffn_workspace(P, H, I);
+  if (!workspace || ws_bytes < need)
+    return set_error(MOE_EWORKSPACE, "moe_q4_grouped_ffn: workspace of %zu bytes, %zu needed", ws_bytes, need);
+  REQUIRE(aligned(workspace, 256), "moe_q4_grouped_ffn: workspace must be 256-byte aligned");
+  _Float16* xs = (_Float16*)workspace;
+  _Float16* act = (_Float16*)((char*)workspace + align256((size_t)P * H * 2));
+  return grouped_ffn(x, ldx, reinterpret_cast<const ExpertDesc*>(table), nexp, eoff, rows, P, H, I, gs, xs, act, y, ldy,
+                     as_stream(stream));
+}
+
+MOE_API size_t moe_prefill_workspace(int T, int E, int k, int H, int I) {
+  if (T <= 0 || E <= 0 || k <= 0 || H <= 0 || I <= 0) return 0;
+  const int pass = T < max_group_tokens(E) ? T : max_group_tokens(E);
+  return prefill_layout(nullptr, pass, E, k, H, I).bytes;
+}
+
+MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int T, int E, int k, int normalize,
+                              const moe_q4_expert* table, int H, int I, int gs, float* out, int ldo, void* workspace,
+                              size_t ws_bytes, void* stream) {
+  if (int rc = check_mfma_shape("moe_prefill_layer", H, I, gs)) return rc;
+  REQUIRE(E > 0 && E <= 256 && k > 0 && k <= E && k <= 16, "moe_prefill_layer: E=%d k=%d (E <= 256, k <= 16)", E, k);
+  REQUIRE(T >= 0 && ldx >= H && ldo >= H, "moe_prefill_layer: T=%d ldx=%d ldo=%d", T, ldx, ldo);
+  if (T == 0) return MOE_OK;
+  REQUIRE(x && router && table && out, "moe_prefill_layer: null pointer");
+  const size_t need = moe_prefill_workspace(T, E, k, H, I);
+  if (!workspace || ws_bytes < need)
+    return set_error(MOE_EWORKSPACE, "moe_prefill_layer: workspace of %zu bytes, %zu needed", ws_bytes, need);
+  REQUIRE(aligned(workspace, 256), "moe_prefill_layer: workspace must be 256-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const ExpertDesc* tab = reinterpret_cast<const ExpertDesc*>(table);
+  const int pass = max_group_tokens(E);
+  for (int t0 = 0; t0 < T; t0 += pass) {  // passes of at most `pass` tokens, as moelan/model.py:640-666
+    const int n = T - t0 < pass ? T - t0 : pass;
+    PrefillWs w = prefill_layout(workspace, n, E, k, H, I);
+    const float* xp = x + (size_t)t0 * ldx;
+    int rc = run_router_logits(xp, ldx, router, n, E, H, w.logits, st);
+    if (!rc) rc = run_route(w.logits, n, E, k, normalize, w.idx, w.w, st);
+    if (!rc) rc = run_group(w.idx, w.w, n, k, E, w.eoff, w.rows, w.wts, w.pos, w.experts, w.offsets, w.n_used, st);
+    if (!rc) rc = grouped_ffn(xp, ldx, tab, E, w.eoff, w.rows, n * k, H, I, gs, w.xs, w.act, w.y, H, st);
+    if (!rc) rc = run_token_combine(w.y, H, w.pos, w.wts, n, k, H, out + (size_t)t0 * ldo, ldo, st);
+    if (rc) return rc;
+  }
+  return MOE_OK;
+}
+
+MOE_API size_t moe_q4_gemm_workspace(int n, int I) {
+  if (n <= 0 || I <= 0) return 0;
+  return align256((size_t)n * I * 2);
+}
+
+MOE_API int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs,
+                        int offset, float* y, void* workspace, size_t ws_bytes, void* stream) {
+  REQUIRE(O > 0 && I > 0 && I % 128 == 0, "moe_q4_gemm: O=%d, I=%d must be a multiple of 128", O, I);
+  REQUIRE(gs > 0 && gs % 32 == 0 && I % gs == 0, "moe_q4_gemm: group size %d must be a multiple of 32 dividing I=%d",
+          gs, I);
+  REQUIRE(n >= 0, "moe_q4_gemm: n=%d", n);
+  if (n == 0) return MOE_OK;
+  REQUIRE(x && raw && s && y, "moe_q4_gemm: null pointer");
+  const size_t need = moe_q4_gemm_workspace(n, I);
+  if (!workspace || ws_bytes < need)
+    return set_error(MOE_EWORKSPACE, "moe_q4_gemm: workspace of %zu bytes, %zu needed", ws_bytes, need);
+  REQUIRE(aligned(workspace, 256), "moe_q4_gemm: workspace must be 256-byte aligned");
+  hipStream_t st = as_stream(stream);
+  _Float16* xs = (_Float16*)workspace;
+  int rc = run_gather_f16(x, I, nullptr, n, I, xs, st);
+  if (rc) return rc;
+  GemmArgs g{};
+  g.A = xs;
+  g.lda = I;
+  g.table = nullptr;
+  g.single = ExpertDesc{raw, s, nullptr, nullptr, offset ? 0u : 0x88u, s_f16};
+  g.single_rows = n;
+  g.which = 0;
+  g.K = I;
+  g.N = O;
+  g.gs = gs;
+  g.Y = y;
+  g.ldy = O;
+  return run_gemm(MODE_PLAIN, g, 1, st);
 }

@@ -1,0 +1,37 @@
+#pragma once
+#include "common.h"
+#include "matvec.h"
+
+namespace moe {
+
+enum { MODE_PLAIN = 0, MODE_GATE_UP = 1, MODE_DOWN = 2 };
+
+struct GemmArgs {
+  const _Float16* A;  // [P, K] activations, f16, 8-column groups in MFMA order
+  int lda;
+  const int* eoff;           // [nexp + 1] rows of expert e: eoff[e] .. eoff[e+1]
+  const ExpertDesc* table;   // expert e's matrices; null: `single` with rows 0 .. single_rows
+  ExpertDesc single;
+  int single_rows;
+  int which;                 // 0: gate|up, 1: down
+  int K;                     // reduction length (H for gate|up, I for down)
+  int N;                     // output columns (PLAIN / DOWN)
+  int I;                     // intermediate size (GATE_UP: up rows start at I)
+  int gs;
+  float* Y;  // PLAIN / DOWN output [P, N] f32
+  int ldy;
+  _Float16* act;  // GATE_UP output [P, I] f16, MFMA column order
+  int ldact;
+};
+
+int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, hipStream_t st);
+int run_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st);
+size_t group_lds_bytes(int T, int E);
+int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
+              int* experts, int* offsets, int* n_used, hipStream_t st);
+int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, hipStream_t st);
+int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st);
+int run_token_combine(const float* y, int ldy, const int* pos, const float* wts, int T, int k, int H, float* out,
+                      int ldo, hipStream_t st);
+
+}  // namespace moe

@@ -219,15 +219,20 @@ class ExpertStore:
         self.hits += 1
         return e
 
-    def compute(self, layer: int, x, groups):
-        """Weighted sum of the routed experts' outputs for the given rows.
-        ``groups``: (expert, rows, weights) per expert. int4 experts run in one
-        fused layer call; others one after another. Returns the type of ``x``."""
+    def compute(self, layer: int, x, groups, mfma: bool = True):
+        """Weighted sum of the routed experts' outputs for the given rows
+        (moelan/experts.py:641-670). ``groups``: (expert, rows, weights) per
+        expert. int4 experts with at least ``kernels.MFMA_FROM`` rows (prompt
+        reading) run as one grouped MFMA GEMM (f16 operands); the other int4
+        experts as one fused f32 layer call; other formats one by one. All
+        weighted sums go through the deterministic combine kernel. Returns the
+        type of ``x``."""
         import torch
         groups = list(groups)
         xd = kernels.to_device(x, torch.float32)
         out = torch.zeros(xd.shape, dtype=torch.float32, device=xd.device)
         items, H, shape = [], xd.shape[1], None
+        big = []
         ys, yrows, yw = [], [], []
         for expert, rows, weights in groups:
             e = self.get((layer, int(expert)))
@@ -235,6 +240,10 @@ class ExpertStore:
                 ok = isinstance(e.gu, Packed4) and isinstance(e.down, Packed4)
                 e.fused = (kernels.q4_expert_ptrs(e) if ok else None) or False
             dims = (e.inter, e.gu.gs) if e.fused else None
+            if (mfma and e.fused and len(rows) >= kernels.MFMA_FROM and H % 128 == 0 and e.inter % 128 == 0
+                    and e.gu.gs % 32 == 0):
+                big.append((e, rows, weights))
+                continue
             if kernels.FUSED and e.fused and (shape is None or dims == shape):
                 shape = dims
                 items.append((e.fused, rows, weights))
@@ -243,7 +252,21 @@ class ExpertStore:
             ys.append(e(xd.index_select(0, rows_t)))
             yrows.append(rows)
             yw.append(weights)
+        for inter, gs in sorted({(e.inter, e.gu.gs) for e, _, _ in big}):
+            sel = [(e, r, w) for e, r, w in big if (e.inter, e.gu.gs) == (inter, gs)]
+            table = kernels.expert_table([e for e, _, _ in sel])
+            eoff = np.zeros(len(sel) + 1, np.int32)
+            np.cumsum([len(r) for _, r, _ in sel], out=eoff[1:])
+            rows_all = np.concatenate([np.asarray(r, np.int32) for _, r, _ in sel])
+            y = kernels.grouped_ffn(xd, table, eoff, rows_all, H, inter, gs)
+            ys.append(y)
+            yrows.append(rows_all)
+            yw.append(np.concatenate([np.asarray(w, np.float32) for _, _, w in sel]))
         kernels.combine(out, ys, yrows, yw)
         if items:
             kernels.moe_q4(xd, items, H, shape[0], shape[1], out)
         return out if kernels.is_device(x) else out.cpu().numpy()
+
+    def layer_table(self, layer: int, num_experts: int):
+        """Device table of all int4 experts of a layer (expert id -> descriptor), for the prefill layer call."""
+        return kernels.expert_table([self.get((layer, e)) for e in range(num_experts)])

@@ -357,3 +357,127 @@ def moe_q4_run(x, meta: LayerMeta, H: int, I: int, gs: int, out, workspace=None)
               meta.max_rows, _ptr(ws), ws.numel(), stream_handle())
     if od is not out:
         _into(out, od)
+
+
+# ---------------------------------------------------------------- prompt reading
+
+MFMA_FROM = 16   # rows per expert from which the store uses the MFMA grouped GEMM (f16 operands)
+
+
+def _i32(a):
+    return to_device(a, torch.int32)
+
+
+def router_logits(x, router):
+    """logits = x @ router.T in f32 on the device (moelan/model.py:597)."""
+    _need()
+    xd, rd = _f32(x), _f32(router)
+    T, H = xd.shape
+    E = rd.shape[0]
+    if rd.shape[1] != H:
+        raise ValueError(f"router has {rd.shape[1]} columns, x {H}")
+    out = torch.empty((T, E), dtype=torch.float32, device=xd.device)
+    _lib.call("moe_router_logits", _ptr(xd), H, _ptr(rd), T, E, H, _ptr(out), stream_handle())
+    return _ret(out, x)
+
+
+def route(logits, top_k: int, normalize: bool):
+    """Softmax top-k router (moelan/model.py:160-167): (idx int32 (n,k), w f32 (n,k))."""
+    _need()
+    ld = _f32(logits)
+    T, E = ld.shape
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=ld.device)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=ld.device)
+    _lib.call("moe_route", _ptr(ld), T, E, int(top_k), 1 if normalize else 0, _ptr(idx), _ptr(w), stream_handle())
+    return (idx, w) if is_device(logits) else (idx.cpu().numpy(), w.cpu().numpy())
+
+
+def group_by_expert(idx, w, num_experts: int | None = None, with_pos: bool = False):
+    """Stable grouping by expert (moelan/model.py:226-236): experts, offsets, rows, weights.
+    ``num_experts`` bounds the expert ids (default: max id + 1)."""
+    _need()
+    idd, wd = _i32(idx), _f32(w)
+    T, k = idd.shape
+    E = int(num_experts) if num_experts is not None else int(idd.max().item()) + 1
+    dev = idd.device
+    eoff = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    rows = torch.empty(T * k, dtype=torch.int32, device=dev)
+    wts = torch.empty(T * k, dtype=torch.float32, device=dev)
+    pos = torch.empty(T * k, dtype=torch.int32, device=dev)
+    experts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    n_used = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("moe_group_by_expert", _ptr(idd), _ptr(wd), T, k, E, _ptr(eoff), _ptr(rows), _ptr(wts), _ptr(pos),
+              _ptr(experts), _ptr(offsets), _ptr(n_used), stream_handle())
+    nu = int(n_used.item())
+    res = (experts[:nu], offsets[:nu + 1], rows, wts)
+    if not is_device(idx):
+        res = tuple(t.cpu().numpy() for t in res)
+    if with_pos:
+        return res + ((eoff, pos),)
+    return res
+
+
+def expert_table(experts) -> "torch.Tensor":
+    """A device array of moe_q4_expert descriptors for int4 experts (None entries: zeros)."""
+    table = (_lib.Q4Expert * max(len(experts), 1))()
+    for i, e in enumerate(experts):
+        if e is None:
+            continue
+        p = q4_expert_ptrs(e)
+        if p is None:
+            raise ValueError(f"expert {i} is not an int4 expert with matching gate|up / down layout")
+        if any(a % 16 for a in p[:4]):
+            raise ValueError(f"expert {i}: weight arrays must be 16-byte aligned in HBM")
+        table[i] = _lib.Q4Expert(*p)
+    return to_device(np.frombuffer(bytes(table), np.uint8).copy())
+
+
+def grouped_ffn(x, table, eoff, rows, H: int, I: int, gs: int):
+    """y[q] = expert_e(x[rows[q]]) for each grouped row (MFMA path, f16 operands)."""
+    _need()
+    xd = _f32(x)
+    eo, rw = _i32(eoff), _i32(rows)
+    P = rw.numel()
+    nexp = eo.numel() - 1
+    y = torch.empty((P, H), dtype=torch.float32, device=xd.device)
+    if P == 0:
+        return y
+    need = _lib.lib().moe_q4_grouped_ffn_workspace(P, H, I)
+    ws = torch.empty(need, dtype=torch.uint8, device=xd.device)
+    _lib.call("moe_q4_grouped_ffn", _ptr(xd), xd.shape[1], _ptr(table), nexp, _ptr(eo), _ptr(rw), P, H, I, gs,
+              _ptr(y), H, _ptr(ws), ws.numel(), stream_handle())
+    return y
+
+
+def prefill_layer(x, router, table, top_k: int, normalize: bool, H: int, I: int, gs: int, out=None, workspace=None):
+    """One MoE layer over x's rows on the device: router, route, group, grouped
+    expert FFN, weighted combine (MoEModel._ffn + LocalBackend + ExpertStore.compute)."""
+    _need()
+    xd, rd = _f32(x), _f32(router)
+    T = xd.shape[0]
+    E = rd.shape[0]
+    od = out if out is not None else torch.empty((T, H), dtype=torch.float32, device=xd.device)
+    need = _lib.lib().moe_prefill_workspace(T, E, top_k, H, I)
+    ws = workspace if workspace is not None and workspace.numel() >= need else \
+        torch.empty(need, dtype=torch.uint8, device=xd.device)
+    _lib.call("moe_prefill_layer", _ptr(xd), xd.shape[1], _ptr(rd), T, E, int(top_k), 1 if normalize else 0,
+              _ptr(table), H, I, gs, _ptr(od), od.shape[1], _ptr(ws), ws.numel(), stream_handle())
+    return od if is_device(x) else od.cpu().numpy()
+
+
+def q4_matmul_t_mfma(x, raw, s, gs: int, offset: bool):
+    """x @ W.T for int4 bytes on many rows through the f16 MFMA path (~1e-3 relative)."""
+    _need()
+    xd = _f32(x)
+    rd, sd = to_device(raw, torch.uint8), to_device(s)
+    n, I = xd.shape
+    O = rd.shape[0]
+    if rd.numel() != O * (I // 2) or sd.numel() != O * (I // gs):
+        raise ValueError("int4 matrix does not match x")
+    y = torch.empty((n, O), dtype=torch.float32, device=xd.device)
+    need = _lib.lib().moe_q4_gemm_workspace(max(n, 1), I)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=xd.device)
+    _lib.call("moe_q4_gemm", _ptr(xd), n, _ptr(rd), _ptr(sd), _scale_kind(sd), O, I, gs, 1 if offset else 0, _ptr(y),
+              _ptr(ws), ws.numel(), stream_handle())
+    return _ret(y, x)

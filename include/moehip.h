@@ -138,6 +138,58 @@ int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4
                           int k, const int* poff, int which, int H, int I, int gs, int max_rows, float* y, int ldy,
                           void* stream);
 
+/* ------------------------------------------------ prompt reading (prefill) */
+
+/* logits[T, E] = x[T, H] @ router[E, H].T in f32 (the router product of
+ * MoEModel._ffn, moelan/model.py:597). */
+int moe_router_logits(const float* x, int ldx, const float* router, int T, int E, int H, float* logits, void* stream);
+
+/* Softmax router with top-k: idx[T, k] int32, w[T, k] f32, largest first,
+ * ties to the lower expert id; w renormalised to sum 1 when normalize != 0.
+ * E <= 256, k <= 64. Replaces route(), moelan/model.py:154-167 (softmax :83-86). */
+int moe_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, void* stream);
+
+/* Stable grouping of the T*k picks by expert, as group_by_expert(),
+ * moelan/model.py:226-236: experts[0..*n_used) ascending with their pick
+ * ranges offsets[0..*n_used]; eoff[E+1] the same ranges for every expert id;
+ * rows[q] / wts[q] the token and weight of grouped pick q; pos[t*k+j] where
+ * pick j of token t went (-1 for an expert id outside 0..E-1). One pass holds
+ * T <= 65536*8/E tokens. All device arrays. */
+int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
+                        int* experts, int* offsets, int* n_used, void* stream);
+
+/* Bytes of workspace moe_q4_grouped_ffn needs for P grouped rows. */
+size_t moe_q4_grouped_ffn_workspace(int P, int H, int I);
+
+/* y[q] = expert_e(x[rows[q]]) for every grouped row q of every expert e
+ * (rows eoff[e] .. eoff[e+1], expert table[e]): the SwiGLU expert FFN of
+ * Expert.__call__, moelan/experts.py:256-259, on many rows at once, as the
+ * reference's big-group path (dequant + BLAS, moelan/experts.py:216-219,
+ * 718-723). int4 -> f16 in registers, f16 MFMA with f32 accumulation
+ * (relative error ~1e-3 at most). H, I multiples of 128; gs a multiple of 32. */
+int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* table, int nexp, const int* eoff, const int* rows,
+                       int P, int H, int I, int gs, float* y, int ldy, void* workspace, size_t ws_bytes, void* stream);
+
+/* Bytes of workspace moe_prefill_layer needs (one pass of tokens). */
+size_t moe_prefill_workspace(int T, int E, int k, int H, int I);
+
+/* One MoE layer over T tokens: router logits, route, group, grouped expert
+ * FFN, weighted combine; out[t] = sum over t's k experts (ascending id) of
+ * w * expert(x[t]) (written, not added). table[e] is expert e of the layer.
+ * MoEModel._ffn + LocalBackend._moe + ExpertStore.compute for a prompt,
+ * moelan/model.py:597-606, 274-278, moelan/experts.py:641-670. */
+int moe_prefill_layer(const float* x, int ldx, const float* router, int T, int E, int k, int normalize,
+                      const moe_q4_expert* table, int H, int I, int gs, float* out, int ldo, void* workspace,
+                      size_t ws_bytes, void* stream);
+
+/* Bytes of workspace moe_q4_gemm needs for n rows of width I. */
+size_t moe_q4_gemm_workspace(int n, int I);
+
+/* y[n, O] = x[n, I] @ W.T for one int4 matrix on many rows through the f16
+ * MFMA path (Packed4.matmul_t's BLAS branch, moelan/experts.py:216-219). */
+int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs, int offset,
+                float* y, void* workspace, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,187 @@
+"""Prompt reading on the GPU against the oracle: router product, routing and
+grouping (indices bit-exact), the grouped f16-MFMA expert FFN and a whole
+Qwen3-30B-A3B-shaped MoE layer (T=512, 128 experts, top-8) within 2e-3
+relative (norm-wise per token; TOL below)."""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from distributedmoellm_amd import experts as X
+from distributedmoellm_amd import model as M
+from oracle import restate as R
+
+from test_layer_gpu import oracle_expert
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def close_rows(got, ref, tol=TOL, rows=None):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape and np.all(np.isfinite(got))
+    sel = range(ref.shape[0]) if rows is None else rows
+    worst = 0.0
+    for r in sel:
+        e = np.linalg.norm(got[r] - ref[r]) / max(np.linalg.norm(ref[r]), 1e-30)
+        worst = max(worst, e)
+    assert worst <= tol, f"worst per-row relative error {worst:.3e} > {tol}"
+    return worst
+
+
+# ---------------------------------------------------------------- router
+
+def test_router_logits(kernels):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((512, 2048)).astype(np.float32)
+    Rw = (rng.standard_normal((128, 2048)) * 0.02).astype(np.float32)
+    got = kernels.router_logits(x, Rw)
+    ref = x.astype(np.float64) @ Rw.T.astype(np.float64)
+    assert np.linalg.norm(got - ref) <= 1e-6 * np.linalg.norm(ref)
+
+
+def test_route_literal(kernels):
+    """The reference's known answer (tests/test_moelan.py:64-72), on the device."""
+    g = json.loads((GOLDEN / "route_literal.json").read_text())
+    idx, w = kernels.route(np.array(g["logits"], np.float32), g["top_k"], True)
+    assert idx.tolist() == g["idx"]
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+    experts, offsets, rows, weights = kernels.group_by_expert(idx, w, 4)
+    assert experts.tolist() == g["experts"]
+    assert rows[offsets[2]:offsets[3]].tolist() == g["rows_of_expert_3"]
+
+
+def near_tie_rows(logits, k, rel=4e-7):
+    """Rows whose k-th and (k+1)-th probabilities are within a few ulps (f32
+    softmax rounding may order them either way)."""
+    p = np.sort(R.softmax(logits.astype(np.float32)), axis=1)[:, ::-1]
+    gap = (p[:, k - 1] - p[:, k]) / np.maximum(p[:, k - 1], 1e-30)
+    return set(np.nonzero(gap < rel)[0].tolist())
+
+
+@pytest.mark.parametrize("E,k", [(128, 8), (64, 4), (256, 8), (8, 2), (60, 6)])
+def test_route_matches_oracle_on_identical_logits(kernels, E, k):
+    rng = np.random.default_rng(E + k)
+    logits = rng.standard_normal((700, E)).astype(np.float32) * 2
+    logits[3] = 0.25                        # all tied: lowest ids win
+    logits[7, : min(E, 12)] = 3.0           # ties among the winners
+    for normalize in (True, False):
+        idx, w = kernels.route(logits, k, normalize)
+        ridx, rw = R.route(logits, k, normalize)
+        ties = near_tie_rows(logits, k)
+        ok = [r for r in range(len(logits)) if r not in ties]
+        assert np.array_equal(idx[ok], ridx[ok])
+        assert idx[3].tolist() == list(range(k))
+        np.testing.assert_allclose(w[ok], rw[ok], rtol=2e-6, atol=1e-7)
+        assert len(ties) <= 2
+
+
+@pytest.mark.parametrize("T,k,E", [(512, 8, 128), (1792, 8, 128), (37, 4, 16), (1, 2, 8)])
+def test_group_by_expert_bit_exact(kernels, T, k, E):
+    rng = np.random.default_rng(T)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    got = kernels.group_by_expert(torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), E, with_pos=True)
+    experts, offsets, rows, weights = (t.cpu().numpy() for t in got[:4])
+    eoff, pos = (t.cpu().numpy() for t in got[4])
+    re, ro, rr, rwt = R.group_by_expert(idx, w)
+    assert np.array_equal(experts, re) and np.array_equal(offsets, ro)
+    assert np.array_equal(rows, rr) and np.array_equal(weights, rwt)
+    assert eoff[-1] == T * k
+    flat = idx.reshape(-1)
+    assert np.array_equal(rows[pos], np.arange(T * k) // k)
+    assert np.array_equal(weights[pos], w.reshape(-1))
+    assert np.all(np.diff(eoff) >= 0) and np.array_equal(np.diff(eoff)[re], np.diff(ro))
+    assert np.array_equal(np.bincount(flat, minlength=E), np.diff(eoff))
+
+
+def test_group_pass_limit_is_an_error(kernels):
+    idx = np.zeros((4000, 8), np.int32) + np.arange(8, dtype=np.int32)
+    with pytest.raises(RuntimeError, match="exceed one pass"):
+        kernels.group_by_expert(idx, np.ones((4000, 8), np.float32), 128)
+
+
+# ---------------------------------------------------------------- grouped expert FFN
+
+@pytest.fixture(scope="module")
+def c4_experts():
+    """128 Qwen3-30B-A3B-shaped int4 experts (H=2048, I=768, gs=32, f16 scales)."""
+    rng = np.random.default_rng(42)
+    return [X.synthetic_expert(2048, 768, "int4", 32, rng) for _ in range(128)]
+
+
+def test_grouped_ffn_matches_oracle(kernels, c4_experts):
+    rng = np.random.default_rng(1)
+    sizes = [1, 5, 16, 33, 64, 100, 0, 7]
+    ex = c4_experts[:len(sizes)]
+    x = rng.standard_normal((120, 2048)).astype(np.float32)
+    rows = [np.sort(rng.choice(120, n, replace=False)).astype(np.int32) for n in sizes]
+    eoff = np.zeros(len(sizes) + 1, np.int32)
+    np.cumsum(sizes, out=eoff[1:])
+    table = kernels.expert_table(ex)
+    y = kernels.grouped_ffn(x, table, eoff, np.concatenate(rows), 2048, 768, 32).cpu().numpy()
+    for i, e in enumerate(ex):
+        if sizes[i] == 0:
+            continue
+        ref = R.expert_exact(x[rows[i]], *oracle_expert(e))
+        close_rows(y[eoff[i]:eoff[i + 1]], ref)
+
+
+@pytest.mark.parametrize("O,I,n", [(1536, 2048, 64), (2048, 768, 40), (256, 128, 17)])
+def test_q4_gemm_mfma(kernels, O, I, n):
+    rng = np.random.default_rng(O + n)
+    raw = rng.integers(0, 256, (O, I // 2), dtype=np.uint8)
+    s = (np.abs(rng.normal(0, 0.02, (O, I // 32))) / 8).astype(np.float16)
+    x = rng.standard_normal((n, I)).astype(np.float32)
+    close_rows(kernels.q4_matmul_t_mfma(x, raw, s, 32, False), R.q4_matmul_t(x, raw, s, 32, False))
+
+
+# ---------------------------------------------------------------- whole layer
+
+def test_qwen3_30b_prefill_layer(kernels, c4_experts):
+    """One Qwen3-30B-A3B-shaped MoE layer, T=512 prompt tokens, 128 experts, top-8."""
+    rng = np.random.default_rng(7)
+    T, H, I, E, k = 512, 2048, 768, 128, 8
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    Rw = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    table = kernels.expert_table(c4_experts)
+    out = kernels.prefill_layer(x, Rw, table, k, True, H, I, 32)
+    # the oracle routes on the device's logits (routing is checked separately)
+    logits = kernels.router_logits(x, Rw)
+    ridx, rw = R.route(logits, k, True)
+    gidx, _ = kernels.route(logits, k, True)
+    ties = near_tie_rows(logits, k)
+    assert len(ties) <= 2
+    ok = [t for t in range(T) if t not in ties and np.array_equal(gidx[t], ridx[t])]
+    assert len(ok) >= T - 2
+    ref = np.zeros((T, H))
+    for e in range(E):
+        sel = np.nonzero((ridx == e).any(1))[0]
+        if len(sel) == 0:
+            continue
+        we = rw[sel, np.argmax(ridx[sel] == e, axis=1)].astype(np.float64)
+        ref[sel] += R.expert_exact(x[sel], *oracle_expert(c4_experts[e])) * we[:, None]
+    worst = close_rows(out, ref, rows=ok)
+    print(f"prefill layer worst per-token relative error {worst:.2e}")
+
+
+def test_store_and_backend_prefill(kernels):
+    """ExpertStore.compute with big groups (MFMA) and small ones (fused f32), via LocalBackend."""
+    rng = np.random.default_rng(9)
+    H, I, E, k, T = 256, 128, 16, 4, 96
+    ex = {(0, e): X.synthetic_expert(H, I, "int4", 32, rng) for e in range(E)}
+    store = X.ExpertStore(ex)
+    backend = M.LocalBackend(store)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[:, 0] += 3.0     # expert 0 gets most tokens (MFMA path), others few
+    idx, w = R.route(logits, k, True)
+    got = backend.moe(0, x, idx, w)
+    want = R.store_compute(x, R.groups_of(idx, w), lambda e, xr: R.expert_exact(xr, *oracle_expert(ex[(0, e)])))
+    close_rows(got, want)
+    assert backend.heat[(0, 0)] == int((idx == 0).sum())
