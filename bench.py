@@ -288,6 +288,88 @@ def stack_decode(args, L):
     return res
 
 
+def prefill_c4(args, L):
+    """Qwen3-30B-A3B-shaped MoE layer prefill: T=512 tokens, 128 experts (H=2048,
+    I=768, int4 g32, f16 scales), f32 router, softmax top-8 renormalised. Four
+    layers' experts (1.36 GB) are cycled so each step streams its 340 MB of
+    expert weights from HBM rather than the 256 MB MALL."""
+    import torch
+    T, H, I, gs, E, k, nlayers = 512, 2048, 768, 32, 128, 8, 4
+    pools = [Int4Pool(E, H, I, gs, seed=200 + l) for l in range(nlayers)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    routers = [torch.randn((E, H), device="cuda", generator=g) * 0.02 for _ in range(nlayers)]
+    x = torch.randn((T, H), device="cuda", generator=g)
+    out = torch.empty((T, H), device="cuda")
+    need = L.moe_prefill_workspace(T, E, k, H, I)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        l = i % nlayers
+        rc = L.moe_prefill_layer(x.data_ptr(), H, routers[l].data_ptr(), T, E, k, 1, pools[l].table.data_ptr(), H, I,
+                                 gs, out.data_ptr(), H, ws.data_ptr(), ws.numel(), stream)
+        if rc:
+            from distributedmoellm_amd import _lib
+            raise RuntimeError(_lib.last_error())
+    for i in range(max(args.warmup, nlayers)):
+        step(i)
+    torch.cuda.synchronize()
+    steps = max(8, args.steps)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        evs[i][0].record()
+        step(i)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) / steps * 1e3
+    ev_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    flops = T * k * 2 * 3 * H * I + 2 * T * H * E
+    wbytes = E * expert_bytes(H, I, gs)
+    res = dict(ms_per_layer=ev_ms, wall_ms_per_layer=wall_ms, tokens_per_s=T / (ev_ms / 1e3),
+               tflops=flops / (ev_ms / 1e3) / 1e12, mfma_frac=flops / (ev_ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS,
+               hbm_gbs=(wbytes + 2 * T * H * 4) / (ev_ms / 1e3) / 1e9,
+               hbm_frac=(wbytes + 2 * T * H * 4) / (ev_ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+               hbm_floor_us=wbytes / (HBM_PEAK_GBS * 1e9) * 1e6, mfma_floor_us=flops / (BF16_PEAK_TFLOPS * 1e12) * 1e6,
+               config="T=512, 128 experts H=2048 I=768 int4 g32 f16 scales, top-8 softmax renormalised, "
+                      "f16 MFMA operands with f32 accumulation")
+    res["attainable_frac"] = max(res["hbm_floor_us"], res["mfma_floor_us"]) / (ev_ms * 1e3)
+    del pools
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline_prefill(seconds: float = 6.0):
+    """The reference's prompt path restated on the host: per expert, widen the
+    int4 matrix to f32 and multiply with BLAS (numpy), as moelan/experts.py:216-219
+    with moelan/kernels.py:971-973; a bounded sample of experts."""
+    from oracle import restate as R
+    H, I, gs, rows = 2048, 768, 32, 32
+    rng = np.random.default_rng(3)
+    n, t0 = 0, time.perf_counter()
+    x = rng.standard_normal((rows, H)).astype(np.float32)
+    mats = [(rng.integers(0, 256, (2 * I, H // 2), dtype=np.uint8),
+             (np.abs(rng.normal(0, 0.02, (2 * I, H // gs))) / 8).astype(np.float32),
+             rng.integers(0, 256, (H, I // 2), dtype=np.uint8),
+             (np.abs(rng.normal(0, 0.02, (H, I // gs))) / 8).astype(np.float32)) for _ in range(4)]
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        gr, gsc, dr, dsc = mats[n % 4]
+        h = x @ R.q4_dequant(gr, gsc, gs, False).T
+        a = h[:, :I] / (1 + np.exp(-h[:, :I])) * h[:, I:]
+        _ = a @ R.q4_dequant(dr, dsc, gs, False).T
+        n += 1
+    dt = time.perf_counter() - t0
+    per_expert = dt / n
+    # a layer of 512 tokens x top-8 = 4096 rows over 128 experts, 32 rows each
+    layer_s = per_expert * 128
+    return dict(tokens_per_s=512 / layer_s, layer_ms=layer_s * 1e3, experts_timed=n,
+                threads=os.environ.get("OMP_NUM_THREADS") or str(len(os.sched_getaffinity(0))),
+                kind="port", sample=f"{n} experts x 32 rows: numpy widen (oracle q4_dequant) + BLAS x @ W.T, "
+                                    f"scaled to a 128-expert layer")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -295,6 +377,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, prefill (for measurements)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path's kernels run on one MI355X and --gpus {args.gpus} "
@@ -308,6 +391,18 @@ def main() -> int:
     info = _lib.device_info(torch.cuda.current_device())
     log(f"device {info}")
 
+    only = set(filter(None, args.only.split(",")))
+    if only:
+        res = {}
+        if "decode" in only:
+            r = decode384(args, L)
+            r.pop("pool")
+            res["decode"] = r
+        if "prefill" in only:
+            res["prefill"] = prefill_c4(args, L)
+        print(json.dumps(res, default=float))
+        return 0
+
     r = decode384(args, L)
     log(f"decode384: {r['ms_per_step']:.3f} ms/step, {r['value']:.0f} GB/s; kernel {r['kernel']['achieved_gbs']:.0f} GB/s")
     del r["pool"]
@@ -315,11 +410,18 @@ def main() -> int:
     extras = {"per_layer_calls": r.pop("per_layer_calls")}
     if args.stack:
         extras["stack_235b"] = stack_decode(args, L)
+    log("prefill (Qwen3-30B-A3B layer, T=512) ...")
+    pf = prefill_c4(args, L)
+    log(f"prefill: {pf['ms_per_layer'] * 1e3:.1f} us/layer, {pf['tokens_per_s'] / 1e6:.2f} M tok/s, "
+        f"MFMA {pf['mfma_frac'] * 100:.1f}%, HBM {pf['hbm_frac'] * 100:.1f}%")
+    extras["prefill_c4"] = pf
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
         cpu = cpu_baseline_decode()
         log(f"cpu baseline: {cpu['value']:.1f} GB/s on {cpu['cores']} threads")
+        pf["cpu_baseline"] = cpu_baseline_prefill()
+        log(f"cpu prefill baseline: {pf['cpu_baseline']['tokens_per_s']:.0f} tok/s")
     k = r["kernel"]
     line = {
         "metric": "int4 expert mat-vec HBM GB/s (% peak); MoE-layer prefill tokens/sec on 1 GPU",

@@ -49,15 +49,15 @@ SIGNATURES = {
     "moe_combine": (c_int, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     "moe_q4_experts_matvec": (c_int, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
     "moe_q4_layer_workspace": (c_size_t, [_I, _I, _I]),
-    "moe_router_logits": (c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
+    "moe_router_logits_workspace": (c_size_t, [_I, _I, _I]),
+    "moe_router_logits": (c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _Z, _P]),
     "moe_route": (c_int, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "moe_group_by_expert": (c_int, [_P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "moe_q4_grouped_ffn_workspace": (c_size_t, [_I, _I, _I]),
     "moe_q4_grouped_ffn": (c_int, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _Z, _P]),
     "moe_prefill_workspace": (c_size_t, [_I, _I, _I, _I, _I]),
     "moe_prefill_layer": (c_int, [_P, _I, _P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _P, _Z, _P]),
-    "moe_q4_gemm_workspace": (c_size_t, [_I, _I]),
-    "moe_q4_gemm": (c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _Z, _P]),
+    "moe_q4_gemm": (c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "moe_q4_layer": (c_int, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I,
                              _I, _I, _I, _I, _P, _Z, _P]),
 }

@@ -300,7 +300,7 @@ static PrefillWs prefill_layout(void* base, int T, int E, int k, int H, int I) {
     off += align256(n);
     return (char*)base + o;
   };
-  w.logits = (float*)take((size_t)T * E * 4);
+  w.logits = (float*)take((size_t)router_slices(T, E, H) * T * E * 4);
   w.idx = (int*)take(P * 4);
   w.w = (float*)take(P * 4);
   w.eoff = (int*)take(((size_t)E + 1) * 4);
@@ -317,13 +317,22 @@ static PrefillWs prefill_layout(void* base, int T, int E, int k, int H, int I) {
   return w;
 }
 
+// xs: [P, H] f16 scratch for the gathered rows (null: the gate|up product reads
+// the f32 rows through `rows` itself)
 static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nexp, const int* eoff, const int* rows,
                        int P, int H, int I, int gs, _Float16* xs, _Float16* act, float* y, int ldy, hipStream_t st) {
-  int rc = run_gather_f16(x, ldx, rows, P, H, xs, st);
-  if (rc) return rc;
   GemmArgs g{};
-  g.A = xs;
-  g.lda = H;
+  if (xs) {
+    int rc = run_gather_f16(x, ldx, rows, P, H, xs, st);
+    if (rc) return rc;
+    g.A = xs;
+    g.lda = H;
+  } else {
+    g.rows32 = 1;
+    g.X = x;
+    g.ldx = ldx;
+    g.rows = rows;
+  }
   g.eoff = eoff;
   g.table = table;
   g.which = 0;
@@ -332,7 +341,7 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   g.gs = gs;
   g.act = act;
   g.ldact = I;
-  rc = run_gemm(MODE_GATE_UP, g, nexp, st);
+  int rc = run_gemm(MODE_GATE_UP, g, nexp, st);
   if (rc) return rc;
   GemmArgs d{};
   d.A = act;
@@ -356,12 +365,19 @@ static int check_mfma_shape(const char* who, int H, int I, int gs) {
 }
 }  // namespace moe
 
+MOE_API size_t moe_router_logits_workspace(int T, int E, int H) {
+  if (T <= 0 || E <= 0 || H <= 0) return 0;
+  return (size_t)router_slices(T, E, H) * T * E * sizeof(float);
+}
+
 MOE_API int moe_router_logits(const float* x, int ldx, const float* router, int T, int E, int H, float* logits,
-                              void* stream) {
+                              void* workspace, size_t ws_bytes, void* stream) {
   REQUIRE(T >= 0 && E > 0 && H > 0 && ldx >= H, "moe_router_logits: T=%d E=%d H=%d ldx=%d", T, E, H, ldx);
   if (T == 0) return MOE_OK;
   REQUIRE(x && router && logits, "moe_router_logits: null pointer");
-  return run_router_logits(x, ldx, router, T, E, H, logits, as_stream(stream));
+  // with enough workspace the K dimension is split over more workgroups
+  float* scratch = (workspace && ws_bytes >= moe_router_logits_workspace(T, E, H)) ? (float*)workspace : nullptr;
+  return run_router_logits(x, ldx, router, T, E, H, logits, scratch, as_stream(stream));
 }
 
 MOE_API int moe_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, void* stream) {
@@ -370,7 +386,7 @@ MOE_API int moe_route(const float* logits, int T, int E, int k, int normalize, i
   REQUIRE(T >= 0, "moe_route: T=%d", T);
   if (T == 0) return MOE_OK;
   REQUIRE(logits && idx && w, "moe_route: null pointer");
-  return run_route(logits, T, E, k, normalize, idx, w, as_stream(stream));
+  return run_route(logits, 1, T, E, k, normalize, idx, w, as_stream(stream));
 }
 
 MOE_API int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts,
@@ -395,14 +411,15 @@ MOE_API int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* tab
           ldy);
   if (nexp == 0 || P == 0) return MOE_OK;
   REQUIRE(x && table && eoff && rows && y, "moe_q4_grouped_ffn: null pointer");
+  REQUIRE(aligned(x, 16) && ldx % 4 == 0, "moe_q4_grouped_ffn: x rows must be 16-byte aligned");
   const size_t need = moe_q4_grouped_ffn_workspace(P, H, I);
   if (!workspace || ws_bytes < need)
     return set_error(MOE_EWORKSPACE, "moe_q4_grouped_ffn: workspace of %zu bytes, %zu needed", ws_bytes, need);
   REQUIRE(aligned(workspace, 256), "moe_q4_grouped_ffn: workspace must be 256-byte aligned");
   _Float16* xs = (_Float16*)workspace;
   _Float16* act = (_Float16*)((char*)workspace + align256((size_t)P * H * 2));
-  return grouped_ffn(x, ldx, reinterpret_cast<const ExpertDesc*>(table), nexp, eoff, rows, P, H, I, gs, xs, act, y, ldy,
-                     as_stream(stream));
+  return grouped_ffn(x, ldx, reinterpret_cast<const ExpertDesc*>(table), nexp, eoff, rows, P, H, I, gs, xs, act, y,
+                     ldy, as_stream(stream));
 }
 
 MOE_API size_t moe_prefill_workspace(int T, int E, int k, int H, int I) {
@@ -419,6 +436,7 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
   REQUIRE(T >= 0 && ldx >= H && ldo >= H, "moe_prefill_layer: T=%d ldx=%d ldo=%d", T, ldx, ldo);
   if (T == 0) return MOE_OK;
   REQUIRE(x && router && table && out, "moe_prefill_layer: null pointer");
+  REQUIRE(aligned(x, 16) && ldx % 4 == 0, "moe_prefill_layer: x rows must be 16-byte aligned");
   const size_t need = moe_prefill_workspace(T, E, k, H, I);
   if (!workspace || ws_bytes < need)
     return set_error(MOE_EWORKSPACE, "moe_prefill_layer: workspace of %zu bytes, %zu needed", ws_bytes, need);
@@ -430,8 +448,9 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
     const int n = T - t0 < pass ? T - t0 : pass;
     PrefillWs w = prefill_layout(workspace, n, E, k, H, I);
     const float* xp = x + (size_t)t0 * ldx;
-    int rc = run_router_logits(xp, ldx, router, n, E, H, w.logits, st);
-    if (!rc) rc = run_route(w.logits, n, E, k, normalize, w.idx, w.w, st);
+    const int nz = router_slices(n, E, H);
+    int rc = run_router_partials(xp, ldx, router, n, E, H, nz, w.logits, st);
+    if (!rc) rc = run_route(w.logits, nz, n, E, k, normalize, w.idx, w.w, st);
     if (!rc) rc = run_group(w.idx, w.w, n, k, E, w.eoff, w.rows, w.wts, w.pos, w.experts, w.offsets, w.n_used, st);
     if (!rc) rc = grouped_ffn(xp, ldx, tab, E, w.eoff, w.rows, n * k, H, I, gs, w.xs, w.act, w.y, H, st);
     if (!rc) rc = run_token_combine(w.y, H, w.pos, w.wts, n, k, H, out + (size_t)t0 * ldo, ldo, st);
@@ -440,30 +459,20 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
   return MOE_OK;
 }
 
-MOE_API size_t moe_q4_gemm_workspace(int n, int I) {
-  if (n <= 0 || I <= 0) return 0;
-  return align256((size_t)n * I * 2);
-}
-
 MOE_API int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs,
-                        int offset, float* y, void* workspace, size_t ws_bytes, void* stream) {
+                        int offset, float* y, void* stream) {
   REQUIRE(O > 0 && I > 0 && I % 128 == 0, "moe_q4_gemm: O=%d, I=%d must be a multiple of 128", O, I);
   REQUIRE(gs > 0 && gs % 32 == 0 && I % gs == 0, "moe_q4_gemm: group size %d must be a multiple of 32 dividing I=%d",
           gs, I);
   REQUIRE(n >= 0, "moe_q4_gemm: n=%d", n);
   if (n == 0) return MOE_OK;
   REQUIRE(x && raw && s && y, "moe_q4_gemm: null pointer");
-  const size_t need = moe_q4_gemm_workspace(n, I);
-  if (!workspace || ws_bytes < need)
-    return set_error(MOE_EWORKSPACE, "moe_q4_gemm: workspace of %zu bytes, %zu needed", ws_bytes, need);
-  REQUIRE(aligned(workspace, 256), "moe_q4_gemm: workspace must be 256-byte aligned");
-  hipStream_t st = as_stream(stream);
-  _Float16* xs = (_Float16*)workspace;
-  int rc = run_gather_f16(x, I, nullptr, n, I, xs, st);
-  if (rc) return rc;
+  REQUIRE(aligned(x, 16), "moe_q4_gemm: x must be 16-byte aligned");
   GemmArgs g{};
-  g.A = xs;
-  g.lda = I;
+  g.rows32 = 1;
+  g.X = x;
+  g.ldx = I;
+  g.rows = nullptr;
   g.table = nullptr;
   g.single = ExpertDesc{raw, s, nullptr, nullptr, offset ? 0u : 0x88u, s_f16};
   g.single_rows = n;
@@ -473,5 +482,5 @@ MOE_API int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s
   g.gs = gs;
   g.Y = y;
   g.ldy = O;
-  return run_gemm(MODE_PLAIN, g, 1, st);
+  return run_gemm(MODE_PLAIN, g, 1, as_stream(stream));
 }

@@ -7,8 +7,12 @@ namespace moe {
 enum { MODE_PLAIN = 0, MODE_GATE_UP = 1, MODE_DOWN = 2 };
 
 struct GemmArgs {
-  const _Float16* A;  // [P, K] activations, f16, 8-column groups in MFMA order
+  const _Float16* A;  // [P, K] activations, f16, 8-column groups in MFMA order (rows32 == 0)
   int lda;
+  int rows32;          // activations are f32 rows of X gathered through `rows`
+  const float* X;      // [*, ldx] f32
+  int ldx;
+  const int* rows;     // row of X for each grouped row (null: the grouped row itself)
   const int* eoff;           // [nexp + 1] rows of expert e: eoff[e] .. eoff[e+1]
   const ExpertDesc* table;   // expert e's matrices; null: `single` with rows 0 .. single_rows
   ExpertDesc single;
@@ -24,8 +28,13 @@ struct GemmArgs {
   int ldact;
 };
 
-int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, hipStream_t st);
-int run_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st);
+int router_slices(int T, int E, int H);
+int run_router_partials(const float* x, int ldx, const float* R, int T, int E, int H, int nz, float* part,
+                        hipStream_t st);
+// scratch: router_slices(T, E, H) * T * E floats, or null for one slice
+int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, float* scratch,
+                      hipStream_t st);
+int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st);
 size_t group_lds_bytes(int T, int E);
 int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
               int* experts, int* offsets, int* n_used, hipStream_t st);

@@ -32,47 +32,51 @@ __host__ __device__ inline int perm_pos(int c) { return (c & ~7) | (2 * (c & 3) 
 
 // ------------------------------------------------------------------ router logits
 
-// logits[t, e] = sum_k x[t, k] * R[e, k], f32; 64x64 tiles, K through LDS.
+// Partial logits over one K slice: part[z][t][e] = sum over k in slice z of
+// x[t, k] * R[e, k], f32; 32x32 tiles, 2x2 outputs per thread, K through LDS.
+// Slices are summed in slice order afterwards (deterministic).
 __global__ __launch_bounds__(256) void router_logits_kernel(const float* x, int ldx, const float* R, int T, int E, int H,
-                                                            float* logits) {
-  __shared__ float xs[32][65];
-  __shared__ float rs[32][65];
-  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+                                                            int kslice, float* part) {
+  __shared__ float xs[32][33];
+  __shared__ float rs[32][33];
+  const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32, z = blockIdx.z;
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+  const int kb = z * kslice, ke = min(H, kb + kslice);
+  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  for (int k0 = kb; k0 < ke; k0 += 32) {
+    for (int i = threadIdx.x; i < 32 * 32; i += 256) {
       const int r = i / 32, kk = i % 32, k = k0 + kk;
-      xs[kk][r] = (t0 + r < T && k < H) ? x[(size_t)(t0 + r) * ldx + k] : 0.f;
-      rs[kk][r] = (e0 + r < E && k < H) ? R[(size_t)(e0 + r) * H + k] : 0.f;
+      xs[kk][r] = (t0 + r < T && k < ke) ? x[(size_t)(t0 + r) * ldx + k] : 0.f;
+      rs[kk][r] = (e0 + r < E && k < ke) ? R[(size_t)(e0 + r) * H + k] : 0.f;
     }
     __syncthreads();
 #pragma unroll 8
     for (int kk = 0; kk < 32; ++kk) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = xs[kk][ty * 4 + i];
-        b[i] = rs[kk][tx * 4 + i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+      const float a0 = xs[kk][ty * 2], a1 = xs[kk][ty * 2 + 1];
+      const float b0 = rs[kk][tx * 2], b1 = rs[kk][tx * 2 + 1];
+      acc[0][0] = fmaf(a0, b0, acc[0][0]);
+      acc[0][1] = fmaf(a0, b1, acc[0][1]);
+      acc[1][0] = fmaf(a1, b0, acc[1][0]);
+      acc[1][1] = fmaf(a1, b1, acc[1][1]);
     }
     __syncthreads();
   }
+  float* dst = part + (size_t)z * T * E;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = t0 + ty * 4 + i, e = e0 + tx * 4 + j;
-      if (t < T && e < E) logits[(size_t)t * E + e] = acc[i][j];
+    for (int j = 0; j < 2; ++j) {
+      const int t = t0 + ty * 2 + i, e = e0 + tx * 2 + j;
+      if (t < T && e < E) dst[(size_t)t * E + e] = acc[i][j];
     }
+}
+
+__global__ void sum_slices_kernel(const float* part, int nz, long n, float* out) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    float v = part[i];
+    for (int z = 1; z < nz; ++z) v += part[(size_t)z * n + i];
+    out[i] = v;
+  }
 }
 
 // ------------------------------------------------------------------ routing
@@ -87,8 +91,8 @@ __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
 // One wave per token: softmax over E <= 256 logits (f32: x - max, exp, / sum),
 // k picks by repeated arg-max (ties to the lower expert id, as a stable
 // descending sort), then w / sum(w) when normalising.
-__global__ __launch_bounds__(256) void route_kernel(const float* logits, int T, int E, int k, int normalize, int* idx,
-                                                    float* w) {
+__global__ __launch_bounds__(256) void route_kernel(const float* logits, int nz, int T, int E, int k, int normalize,
+                                                    int* idx, float* w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -98,7 +102,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* logits, int T, 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane + 64 * j;
-    v[j] = e < E ? lg[e] : -INFINITY;
+    float l = -INFINITY;
+    if (e < E) {
+      l = lg[e];
+      for (int z = 1; z < nz; ++z) l += lg[(size_t)z * T * E + e];  // K slices, in order
+    }
+    v[j] = l;
     m = fmaxf(m, v[j]);
   }
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
@@ -255,17 +264,29 @@ __device__ __forceinline__ float gscale(const void* s, size_t i) {
   else return gptr<float>(s)[i];
 }
 
-// One wave: 32 rows (2 x 16) of an expert's token block against 4 weight
-// sub-tiles of 16 rows; per 128-wide K step a lane reads 16 bytes (32 nibbles)
-// of each weight row and 4 x 16 bytes of each activation row it covers, and
-// issues 4 x 2 x 4 MFMAs.
+// A workgroup computes a 32-row x 64-weight-row output tile of one expert
+// (2 x 16 rows, 4 sub-tiles of 16 weight rows); its 4 waves split K: wave w
+// takes the 128-wide K steps w, w+4, ... and the four partial tiles are added
+// through LDS in wave order at the end (deterministic). No barrier in the K
+// loop; each wave loads its next step's operands while computing the current.
+// Per step a lane reads 16 bytes (32 nibbles) of each of its 4 weight rows,
+// widens them to f16 with the group scale, and issues 4 x 2 x 4 MFMAs.
 //   MODE_PLAIN / MODE_DOWN: sub-tile s = weight rows n0 + 16 s .. ; y f32
 //   MODE_GATE_UP: sub-tiles 0,1 gate rows j0 .. j0+31, 2,3 up rows I + j0 ..;
 //                 act = silu(gate) * up as f16, columns in MFMA order
-template <int MODE, bool SF16>
+// Activations: f16 rows (8-column groups in MFMA order), or f32 rows of X
+// gathered through `rows` and rounded to f16 on load.
+
+struct StepRegs {
+  half8 av[2][4];
+  uint4 b[4];
+  float sc[4];
+};
+
+template <int MODE, bool SF16, bool ROWS32>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
-                                          int m1, int nbase) {
-  const int lane = threadIdx.x & 63, ln = lane & 15, q = lane >> 4;
+                                          int m1, int nbase, f32x4* red) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, q = lane >> 4;
   const int row_bytes = a.K / 2, G = a.K / a.gs;
   int wrow[4];
   bool wok[4];
@@ -281,90 +302,134 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const uint8_t* Wt, 
       wrow[s] = wok[s] ? n : 0;
     }
   }
+  const int nsteps = a.K / 128;
+
   for (int mb = m0; mb < m1; mb += 32) {
-    f32x4 acc[2][4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc[h][s] = f32x4{0.f, 0.f, 0.f, 0.f};
     int arow[2];
     bool aok[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int m = mb + 16 * h + ln;
       aok[h] = m < m1;
-      arow[h] = aok[h] ? m : m0;
+      const int mm = aok[h] ? m : m0;
+      arow[h] = ROWS32 ? (a.rows ? a.rows[mm] : mm) : mm;
     }
-    for (int k0 = 0; k0 < a.K; k0 += 128) {
-      const int kc = k0 + 32 * q;  // this lane's 32-column run
-      uint4 braw[4];
-      float bsc[4];
+    auto load_b = [&](StepRegs& r, int st) {
+      const int kc = st * 128 + 32 * q;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        braw[s] = stream_load16(Wt + (size_t)wrow[s] * row_bytes + kc / 2);
-        bsc[s] = gscale<SF16>(S, (size_t)wrow[s] * G + kc / a.gs);
+        r.b[s] = stream_load16(Wt + (size_t)wrow[s] * row_bytes + kc / 2);
+        r.sc[s] = gscale<SF16>(S, (size_t)wrow[s] * G + kc / a.gs);
       }
-      half8 av[2][4];
+    };
+    auto load_a = [&](StepRegs& r, int st) {
+      const int kc = st * 128 + 32 * q;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const half8* src = reinterpret_cast<const half8*>(a.A + (size_t)arow[h] * a.lda + kc);
+        if constexpr (ROWS32) {
+          const float4* src = reinterpret_cast<const float4*>(a.X + (size_t)arow[h] * a.ldx + kc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          av[h][i] = src[i];
-          if (!aok[h]) av[h][i] = half8{};
+          for (int i = 0; i < 4; ++i) {
+            const float4 lo = src[2 * i], hi = src[2 * i + 1];
+            const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int p = 0; p < 8; ++p) r.av[h][i][p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
+            if (!aok[h]) r.av[h][i] = half8{};
+          }
+        } else {
+          const half8* src = reinterpret_cast<const half8*>(a.A + (size_t)arow[h] * a.lda + kc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) r.av[h][i] = aok[h] ? src[i] : half8{};
         }
       }
+    };
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc[h][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const StepRegs& r) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const __half2 s2 = __float2half2_rn(bsc[s]);
-        const uint32_t wd[4] = {braw[s].x ^ xor4, braw[s].y ^ xor4, braw[s].z ^ xor4, braw[s].w ^ xor4};
+        const __half2 s2 = __float2half2_rn(r.sc[s]);
+        const uint32_t wd[4] = {r.b[s].x ^ xor4, r.b[s].y ^ xor4, r.b[s].z ^ xor4, r.b[s].w ^ xor4};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const half8 bv = widen8(wd[i], s2);
 #pragma unroll
-          for (int h = 0; h < 2; ++h) acc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[h][i], bv, acc[h][s], 0, 0, 0);
+          for (int h = 0; h < 2; ++h)
+            acc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.av[h][i], bv, acc[h][s], 0, 0, 0);
         }
       }
+    };
+    // operands are loaded right before use: holding the next step's operands in
+    // registers costs more occupancy (3 -> 2 or 1 waves per SIMD) than it
+    // hides latency
+    StepRegs r;
+    for (int st = wave; st < nsteps; st += 4) {
+      load_b(r, st);
+      load_a(r, st);
+      compute(r);
     }
-    // D layout: lane holds rows 4q .. 4q+3 of column ln of each 16x16 tile
+    // add the waves' partial tiles in wave order
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = mb + 16 * h + 4 * q + j;
-        if (m >= m1) continue;
-        if (MODE == MODE_GATE_UP) {
+      for (int s = 0; s < 4; ++s) red[((wave * 2 + h) * 4 + s) * 64 + lane] = acc[h][s];
+    __syncthreads();
+    // D layout: lane holds rows 4q .. 4q+3 of column ln of each 16x16 tile
+    auto sum_red = [&](int h, int s) {
+      f32x4 v = red[((0 * 2 + h) * 4 + s) * 64 + lane];
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            if (!wok[s]) continue;
-            const float g = acc[h][s][j], u = acc[h][s + 2][j];
-            const int col = nbase + 16 * s + ln;
-            a.act[(size_t)m * a.ldact + perm_pos(col)] = (_Float16)(silu(g) * u);
+      for (int w = 1; w < 4; ++w) v += red[((w * 2 + h) * 4 + s) * 64 + lane];
+      return v;
+    };
+    if (MODE == MODE_GATE_UP) {
+      if (wave < 2) {
+        const int s = wave;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const f32x4 g = sum_red(h, s), u = sum_red(h, s + 2);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int m = mb + 16 * h + 4 * q + j;
+            if (m < m1 && wok[s]) {
+              const int col = nbase + 16 * s + ln;
+              a.act[(size_t)m * a.ldact + perm_pos(col)] = (_Float16)(silu(g[j]) * u[j]);
+            }
           }
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if (wok[s]) a.Y[(size_t)m * a.ldy + nbase + 16 * s + ln] = acc[h][s][j];
         }
       }
+    } else {
+      const int s = wave;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 v = sum_red(h, s);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = mb + 16 * h + 4 * q + j;
+          if (m < m1 && wok[s]) a.Y[(size_t)m * a.ldy + nbase + 16 * s + ln] = v[j];
+        }
+      }
+    }
+    __syncthreads();  // the next row block reuses the LDS tiles
   }
 }
 
-template <int MODE>
+template <int MODE, bool ROWS32>
 __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
+  __shared__ f32x4 red[4 * 2 * 4 * 64];  // 32 KB: per wave, row half, sub-tile, lane
   const int e = blockIdx.y;
   const int m0 = a.table ? a.eoff[e] : 0, m1 = a.table ? a.eoff[e + 1] : a.single_rows;
   if (m0 >= m1) return;
-  const int wave = threadIdx.x >> 6;
-  const int per_wave = MODE == MODE_GATE_UP ? 32 : 64;
-  const int nbase = (blockIdx.x * 4 + wave) * per_wave;
-  if (nbase >= (MODE == MODE_GATE_UP ? a.I : a.N)) return;
+  const int per_tile = MODE == MODE_GATE_UP ? 32 : 64;
+  const int nbase = blockIdx.x * per_tile;
   const ExpertDesc d = a.table ? a.table[e] : a.single;
   const uint8_t* Wt = a.which ? d.dn_w : d.gu_w;
   const void* S = a.which ? d.dn_s : d.gu_s;
   const uint32_t xor4 = d.xor8 * 0x01010101u;
-  if (d.s_f16) gemm_body<MODE, true>(a, Wt, S, xor4, m0, m1, nbase);
-  else gemm_body<MODE, false>(a, Wt, S, xor4, m0, m1, nbase);
+  if (d.s_f16) gemm_body<MODE, true, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, red);
+  else gemm_body<MODE, false, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, red);
 }
 
 // ------------------------------------------------------------------ combine
@@ -411,14 +476,34 @@ static int blocks_for(long n, int per = 256, int cap = 8192) {
   return (int)(b < 1 ? 1 : (b > cap ? cap : b));
 }
 
-int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, hipStream_t st) {
-  hipLaunchKernelGGL(router_logits_kernel, dim3((T + 63) / 64, (E + 63) / 64), dim3(256), 0, st, x, ldx, R, T, E, H,
-                     logits);
+int router_slices(int T, int E, int H) {
+  const long tiles = (long)((T + 31) / 32) * ((E + 31) / 32);
+  int nz = (int)((512 + tiles - 1) / tiles);  // ~512 workgroups
+  const int maxz = (H + 127) / 128;           // slices of at least 128 columns
+  nz = nz < 1 ? 1 : (nz > maxz ? maxz : nz);
+  return nz > 16 ? 16 : nz;
+}
+
+int run_router_partials(const float* x, int ldx, const float* R, int T, int E, int H, int nz, float* part,
+                        hipStream_t st) {
+  const int kslice = ((H + nz - 1) / nz + 31) / 32 * 32;
+  hipLaunchKernelGGL(router_logits_kernel, dim3((T + 31) / 32, (E + 31) / 32, nz), dim3(256), 0, st, x, ldx, R, T, E,
+                     H, kslice, part);
   return check_launch("router logits");
 }
 
-int run_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st) {
-  hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, T, E, k, normalize, idx, w);
+int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, float* scratch,
+                      hipStream_t st) {
+  const int nz = scratch ? router_slices(T, E, H) : 1;
+  int rc = run_router_partials(x, ldx, R, T, E, H, nz, nz > 1 ? scratch : logits, st);
+  if (rc || nz == 1) return rc;
+  const long n = (long)T * E;
+  hipLaunchKernelGGL(sum_slices_kernel, dim3(blocks_for(n)), dim3(256), 0, st, scratch, nz, n, logits);
+  return check_launch("router logits (slice sum)");
+}
+
+int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st) {
+  hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, nz, T, E, k, normalize, idx, w);
   return check_launch("softmax top-k");
 }
 
@@ -441,14 +526,18 @@ int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Floa
 
 int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
   if (nexp <= 0) return MOE_OK;
-  const int per_wave = mode == MODE_GATE_UP ? 32 : 64;
+  const int per_tile = mode == MODE_GATE_UP ? 32 : 64;
   const int n = mode == MODE_GATE_UP ? a.I : a.N;
-  const int waves = (n + per_wave - 1) / per_wave;
-  dim3 grid((waves + 3) / 4, nexp);
-  switch (mode) {
-    case MODE_PLAIN: hipLaunchKernelGGL(gemm_q4_kernel<MODE_PLAIN>, grid, dim3(256), 0, st, a); break;
-    case MODE_GATE_UP: hipLaunchKernelGGL(gemm_q4_kernel<MODE_GATE_UP>, grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(gemm_q4_kernel<MODE_DOWN>, grid, dim3(256), 0, st, a); break;
+  dim3 grid((n + per_tile - 1) / per_tile, nexp);
+  auto go = [&](auto k) { hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a); };
+  if (a.rows32) {
+    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, true>);
+    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, true>);
+    else return set_error(MOE_EINVAL, "int4 grouped GEMM: the down product takes f16 activations");
+  } else {
+    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, false>);
+    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, false>);
+    else go(gemm_q4_kernel<MODE_DOWN, false>);
   }
   return check_launch("int4 grouped GEMM");
 }

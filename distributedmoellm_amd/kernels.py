@@ -377,7 +377,9 @@ def router_logits(x, router):
     if rd.shape[1] != H:
         raise ValueError(f"router has {rd.shape[1]} columns, x {H}")
     out = torch.empty((T, E), dtype=torch.float32, device=xd.device)
-    _lib.call("moe_router_logits", _ptr(xd), H, _ptr(rd), T, E, H, _ptr(out), stream_handle())
+    need = _lib.lib().moe_router_logits_workspace(T, E, H)
+    ws = torch.empty(max(need, 4), dtype=torch.uint8, device=xd.device)
+    _lib.call("moe_router_logits", _ptr(xd), H, _ptr(rd), T, E, H, _ptr(out), _ptr(ws), ws.numel(), stream_handle())
     return _ret(out, x)
 
 
@@ -476,8 +478,6 @@ def q4_matmul_t_mfma(x, raw, s, gs: int, offset: bool):
     if rd.numel() != O * (I // 2) or sd.numel() != O * (I // gs):
         raise ValueError("int4 matrix does not match x")
     y = torch.empty((n, O), dtype=torch.float32, device=xd.device)
-    need = _lib.lib().moe_q4_gemm_workspace(max(n, 1), I)
-    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=xd.device)
     _lib.call("moe_q4_gemm", _ptr(xd), n, _ptr(rd), _ptr(sd), _scale_kind(sd), O, I, gs, 1 if offset else 0, _ptr(y),
-              _ptr(ws), ws.numel(), stream_handle())
+              stream_handle())
     return _ret(y, x)

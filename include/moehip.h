@@ -140,9 +140,13 @@ int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4
 
 /* ------------------------------------------------ prompt reading (prefill) */
 
+/* Bytes of workspace that let moe_router_logits split H over more workgroups. */
+size_t moe_router_logits_workspace(int T, int E, int H);
+
 /* logits[T, E] = x[T, H] @ router[E, H].T in f32 (the router product of
- * MoEModel._ffn, moelan/model.py:597). */
-int moe_router_logits(const float* x, int ldx, const float* router, int T, int E, int H, float* logits, void* stream);
+ * MoEModel._ffn, moelan/model.py:597). Workspace optional (NULL: one slice). */
+int moe_router_logits(const float* x, int ldx, const float* router, int T, int E, int H, float* logits,
+                      void* workspace, size_t ws_bytes, void* stream);
 
 /* Softmax router with top-k: idx[T, k] int32, w[T, k] f32, largest first,
  * ties to the lower expert id; w renormalised to sum 1 when normalize != 0.
@@ -182,13 +186,11 @@ int moe_prefill_layer(const float* x, int ldx, const float* router, int T, int E
                       const moe_q4_expert* table, int H, int I, int gs, float* out, int ldo, void* workspace,
                       size_t ws_bytes, void* stream);
 
-/* Bytes of workspace moe_q4_gemm needs for n rows of width I. */
-size_t moe_q4_gemm_workspace(int n, int I);
-
 /* y[n, O] = x[n, I] @ W.T for one int4 matrix on many rows through the f16
- * MFMA path (Packed4.matmul_t's BLAS branch, moelan/experts.py:216-219). */
+ * MFMA path (Packed4.matmul_t's BLAS branch, moelan/experts.py:216-219);
+ * x 16-byte aligned. */
 int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs, int offset,
-                float* y, void* workspace, size_t ws_bytes, void* stream);
+                float* y, void* stream);
 
 #ifdef __cplusplus
 }
