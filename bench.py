@@ -17,9 +17,16 @@ launches) timed with HIP events on the launch stream inside the timed region.
 cpu_baseline: the C/OpenMP restatement of the reference's numba kernel
 (oracle/cpuref.c, _moe_q4 loop structure) on the host cores, a bounded sample.
 
-Extras in the same line: the same 384 evaluations as 48 per-layer calls, the
-Qwen3-235B-A22B-shaped resident stack decode (--stack; 94 layers x 128
-experts, 119 GiB) at B = 1, 8, 32 with Zipf(1.1) routing.
+roofline.traffic: HBM bytes per launch of that kernel, read from the counter
+summary committed beside the kernel-trace summary
+(profiles/mv_fast_kernel_int4_decode_384experts.md: rocprofv3 FETCH_SIZE and
+WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain
+device copy of known size); null when that summary is absent.
+
+Extras in the same line: the Qwen3-30B-A3B-shaped MoE layer prefill (T=512)
+with its own CPU baseline; with --per-layer the same 384 evaluations as 48
+per-layer calls; with --stack the Qwen3-235B-A22B-shaped resident stack decode
+(94 layers x 128 experts, 119 GiB) at B = 1, 8, 32 with Zipf(1.1) routing.
 """
 
 from __future__ import annotations
@@ -27,6 +34,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -38,6 +46,17 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+TRAFFIC_SUMMARY = ROOT / "profiles" / "mv_fast_kernel_int4_decode_384experts.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode mat-vec from the committed counter
+    summary (its line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.]+)", TRAFFIC_SUMMARY.read_text(), re.M)
+    except OSError:
+        return None
+    return float(m.group(1)) if m else None
 
 
 def log(msg: str) -> None:
@@ -120,7 +139,7 @@ def run_layer(L, pool, x, out, h, y, c, stream, ev=None):
         raise RuntimeError(_lib.last_error())
 
 
-def decode384(args, L):
+def decode384(args, L, per_layer=False):
     """One token's 48 x 8 expert evaluations per step, C1 expert shape, from a 1024-expert pool."""
     import torch
     H, I, gs, npool, per_step = 2048, 768, 32, 1024, 384
@@ -128,7 +147,7 @@ def decode384(args, L):
     pool = Int4Pool(npool, H, I, gs, seed=1)
     rng = np.random.default_rng(0)
     nvar = 8
-    fused, per_layer = [], []
+    fused, layered = [], []
     for v in range(nvar):
         eidx = np.sort(rng.choice(npool, per_step, replace=False)).astype(np.int32)
         rows = [np.zeros(1, np.int32) for _ in range(per_step)]
@@ -136,8 +155,8 @@ def decode384(args, L):
         fused.append((eidx, rows, ws))
         for l in range(48):
             sl = slice(8 * l, 8 * l + 8)
-            per_layer.append((eidx[sl], rows[sl], ws[sl]))
-    cf, cl = Calls(fused), Calls(per_layer)
+            layered.append((eidx[sl], rows[sl], ws[sl]))
+    cf, cl = Calls(fused), Calls(layered)
     x = torch.randn((1, H), device="cuda")
     out = torch.zeros((1, H), device="cuda")
     h = torch.empty((per_step, 2 * I), device="cuda")
@@ -162,12 +181,16 @@ def decode384(args, L):
     avg_s = (gu_ms.mean() + dn_ms.mean()) / 2 / 1e3
     avg_bytes = (gu_bytes + dn_bytes) / 2
     res = dict(ms_per_step=ms, value=step_bytes / (ms / 1e3) / 1e9, step_bytes=step_bytes,
-               kernel=dict(name="mv_kernel<FmtQ4, 1, 4> (moe_q4_experts_matvec)", launches=2 * args.steps,
+               kernel=dict(name="mv_fast_kernel (int4, moe_q4_experts_matvec: gate|up and down launches)",
+                           launches=2 * args.steps,
                            avg_us=avg_s * 1e6, gate_up_us=float(gu_ms.mean() * 1e3),
                            down_us=float(dn_ms.mean() * 1e3), bytes_per_launch=avg_bytes,
                            achieved_gbs=avg_bytes / avg_s / 1e9,
                            gate_up_gbs=gu_bytes / (gu_ms.mean() / 1e3) / 1e9,
                            down_gbs=dn_bytes / (dn_ms.mean() / 1e3) / 1e9))
+    res["pool"] = pool
+    if not per_layer:
+        return res
     # the same evaluations as 48 per-layer calls of 8 experts (decode as it runs layer by layer)
     torch.cuda.synchronize()
     steps = max(2, args.steps // 2)
@@ -182,7 +205,6 @@ def decode384(args, L):
     torch.cuda.synchronize()
     ms_l = (time.perf_counter() - t0) / steps * 1e3
     res["per_layer_calls"] = dict(ms_per_token=ms_l, gbs=step_bytes / (ms_l / 1e3) / 1e9, calls_per_token=48)
-    res["pool"] = pool
     return res
 
 
@@ -376,8 +398,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
+    ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, prefill (for measurements)")
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, prefill, copy "
+                                                "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path's kernels run on one MI355X and --gpus {args.gpus} "
@@ -400,14 +424,25 @@ def main() -> int:
             res["decode"] = r
         if "prefill" in only:
             res["prefill"] = prefill_c4(args, L)
+        if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
+            import torch
+            a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+            b = torch.empty_like(a)
+            torch.cuda.synchronize()
+            for _ in range(3):
+                b.copy_(a)
+            torch.cuda.synchronize()
+            res["copy_bytes"] = a.numel()
         print(json.dumps(res, default=float))
         return 0
 
-    r = decode384(args, L)
+    r = decode384(args, L, per_layer=args.per_layer)
     log(f"decode384: {r['ms_per_step']:.3f} ms/step, {r['value']:.0f} GB/s; kernel {r['kernel']['achieved_gbs']:.0f} GB/s")
     del r["pool"]
     torch.cuda.empty_cache()
-    extras = {"per_layer_calls": r.pop("per_layer_calls")}
+    extras = {}
+    if "per_layer_calls" in r:
+        extras["per_layer_calls"] = r.pop("per_layer_calls")
     if args.stack:
         extras["stack_235b"] = stack_decode(args, L)
     log("prefill (Qwen3-30B-A3B layer, T=512) ...")
@@ -423,6 +458,7 @@ def main() -> int:
         pf["cpu_baseline"] = cpu_baseline_prefill()
         log(f"cpu prefill baseline: {pf['cpu_baseline']['tokens_per_s']:.0f} tok/s")
     k = r["kernel"]
+    traffic = measured_traffic()
     line = {
         "metric": "int4 expert mat-vec HBM GB/s (% peak); MoE-layer prefill tokens/sec on 1 GPU",
         "value": round(r["value"], 1),
@@ -442,7 +478,7 @@ def main() -> int:
                    "experts_per_step": 384, "rows_per_expert": 1, "bytes_per_step": r["step_bytes"]},
         "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(k["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(k["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": k["name"], "avg_launch_us": round(k["avg_us"], 2),
                      "bytes_per_launch": k["bytes_per_launch"],
                      "gate_up": {"us": round(k["gate_up_us"], 2), "gbs": round(k["gate_up_gbs"], 1)},

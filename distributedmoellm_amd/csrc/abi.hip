@@ -341,7 +341,8 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   g.gs = gs;
   g.act = act;
   g.ldact = I;
-  int rc = run_gemm(MODE_GATE_UP, g, nexp, st);
+  const int hint = nexp > 0 ? (P + nexp - 1) / nexp : P;
+  int rc = run_gemm(MODE_GATE_UP, g, nexp, st, hint);
   if (rc) return rc;
   GemmArgs d{};
   d.A = act;
@@ -354,7 +355,7 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   d.gs = gs;
   d.Y = y;
   d.ldy = ldy;
-  return run_gemm(MODE_DOWN, d, nexp, st);
+  return run_gemm(MODE_DOWN, d, nexp, st, hint);
 }
 
 static int check_mfma_shape(const char* who, int H, int I, int gs) {
@@ -482,5 +483,5 @@ MOE_API int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s
   g.gs = gs;
   g.Y = y;
   g.ldy = O;
-  return run_gemm(MODE_PLAIN, g, 1, as_stream(stream));
+  return run_gemm(MODE_PLAIN, g, 1, as_stream(stream), n);
 }

@@ -80,4 +80,14 @@ __device__ __forceinline__ float group_sum(float v, int width) {
   return v;
 }
 
+// Workgroups are dispatched round-robin over the chip's 8 XCDs (each with its
+// own L2): workgroup b runs on XCD b % 8. Returns the logical index for b so
+// that each XCD receives one contiguous range of logical indices (work that
+// shares operands then shares an L2). A bijection on [0, total).
+__device__ __forceinline__ int xcd_contiguous(int b, int total) {
+  constexpr int kXcds = 8;
+  const int x = b % kXcds, slot = b / kXcds, base = total / kXcds, rem = total % kXcds;
+  return x * base + (x < rem ? x : rem) + slot;
+}
+
 }  // namespace moe

@@ -264,38 +264,34 @@ __device__ __forceinline__ float gscale(const void* s, size_t i) {
   else return gptr<float>(s)[i];
 }
 
-// A workgroup computes a 32-row x 64-weight-row output tile of one expert
-// (2 x 16 rows, 4 sub-tiles of 16 weight rows); its 4 waves split K: wave w
-// takes the 128-wide K steps w, w+4, ... and the four partial tiles are added
-// through LDS in wave order at the end (deterministic). No barrier in the K
-// loop; each wave loads its next step's operands while computing the current.
-// Per step a lane reads 16 bytes (32 nibbles) of each of its 4 weight rows,
-// widens them to f16 with the group scale, and issues 4 x 2 x 4 MFMAs.
+// A workgroup computes an output tile of one expert: up to 64 of its rows
+// (NB = 1 or 2 blocks of 32 = 2 x 16) against 32 weight rows (2 sub-tiles of
+// 16); its 4 waves split K: wave w takes the 128-wide K steps w, w+4, ...,
+// and the partial tiles are added through LDS in wave order at the end
+// (deterministic). There is no barrier in the K loop. Per step a lane reads
+// 16 bytes (32 nibbles) of each of its 2 weight rows, widens them to f16 with
+// the group scale once, and uses them for every row block: 2 x 4 x NB x 2
+// MFMAs. An expert with more rows than one pass holds is done in passes
+// (its weight tile is then read again, from L2).
 //   MODE_PLAIN / MODE_DOWN: sub-tile s = weight rows n0 + 16 s .. ; y f32
-//   MODE_GATE_UP: sub-tiles 0,1 gate rows j0 .. j0+31, 2,3 up rows I + j0 ..;
+//   MODE_GATE_UP: sub-tile 0 = gate rows j0 .. j0+15, 1 = up rows I + j0 ..;
 //                 act = silu(gate) * up as f16, columns in MFMA order
 // Activations: f16 rows (8-column groups in MFMA order), or f32 rows of X
 // gathered through `rows` and rounded to f16 on load.
 
-struct StepRegs {
-  half8 av[2][4];
-  uint4 b[4];
-  float sc[4];
-};
-
-template <int MODE, bool SF16, bool ROWS32>
+template <int MODE, bool SF16, bool ROWS32, int NB>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
                                           int m1, int nbase, f32x4* red) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, q = lane >> 4;
   const int row_bytes = a.K / 2, G = a.K / a.gs;
-  int wrow[4];
-  bool wok[4];
+  int wrow[2];
+  bool wok[2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < 2; ++s) {
     if (MODE == MODE_GATE_UP) {
-      const int j = nbase + 16 * (s & 1) + ln;
+      const int j = nbase + ln;
       wok[s] = j < a.I;
-      wrow[s] = (s < 2 ? 0 : a.I) + (wok[s] ? j : 0);
+      wrow[s] = (s == 0 ? 0 : a.I) + (wok[s] ? j : 0);
     } else {
       const int n = nbase + 16 * s + ln;
       wok[s] = n < a.N;
@@ -303,133 +299,135 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const uint8_t* Wt, 
     }
   }
   const int nsteps = a.K / 128;
+  constexpr int RB = 32 * NB;  // rows per pass
 
-  for (int mb = m0; mb < m1; mb += 32) {
-    int arow[2];
-    bool aok[2];
+  for (int mb = m0; mb < m1; mb += RB) {
+    int arow[NB][2];
+    bool aok[NB][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int m = mb + 16 * h + ln;
-      aok[h] = m < m1;
-      const int mm = aok[h] ? m : m0;
-      arow[h] = ROWS32 ? (a.rows ? a.rows[mm] : mm) : mm;
-    }
-    auto load_b = [&](StepRegs& r, int st) {
-      const int kc = st * 128 + 32 * q;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        r.b[s] = stream_load16(Wt + (size_t)wrow[s] * row_bytes + kc / 2);
-        r.sc[s] = gscale<SF16>(S, (size_t)wrow[s] * G + kc / a.gs);
-      }
-    };
-    auto load_a = [&](StepRegs& r, int st) {
-      const int kc = st * 128 + 32 * q;
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if constexpr (ROWS32) {
-          const float4* src = reinterpret_cast<const float4*>(a.X + (size_t)arow[h] * a.ldx + kc);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float4 lo = src[2 * i], hi = src[2 * i + 1];
-            const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-            for (int p = 0; p < 8; ++p) r.av[h][i][p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
-            if (!aok[h]) r.av[h][i] = half8{};
-          }
-        } else {
-          const half8* src = reinterpret_cast<const half8*>(a.A + (size_t)arow[h] * a.lda + kc);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) r.av[h][i] = aok[h] ? src[i] : half8{};
-        }
+        const int m = mb + 32 * b + 16 * h + ln;
+        aok[b][h] = m < m1;
+        const int mm = aok[b][h] ? m : m0;
+        arow[b][h] = ROWS32 ? (a.rows ? a.rows[mm] : mm) : mm;
       }
-    };
-    f32x4 acc[2][4];
+    f32x4 acc[NB][2][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc[h][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](const StepRegs& r) {
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const __half2 s2 = __float2half2_rn(r.sc[s]);
-        const uint32_t wd[4] = {r.b[s].x ^ xor4, r.b[s].y ^ xor4, r.b[s].z ^ xor4, r.b[s].w ^ xor4};
+        for (int s = 0; s < 2; ++s) acc[b][h][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int st = wave; st < nsteps; st += 4) {
+      const int kc = st * 128 + 32 * q;  // this lane's 32-column run
+      uint4 braw[2];
+      float bsc[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        braw[s] = stream_load16(Wt + (size_t)wrow[s] * row_bytes + kc / 2);
+        bsc[s] = gscale<SF16>(S, (size_t)wrow[s] * G + kc / a.gs);
+      }
+      half8 av[NB][2][4];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (ROWS32) {
+            const float4* src = reinterpret_cast<const float4*>(a.X + (size_t)arow[b][h] * a.ldx + kc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float4 lo = src[2 * i], hi = src[2 * i + 1];
+              const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+              for (int p = 0; p < 8; ++p) av[b][h][i][p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
+              if (!aok[b][h]) av[b][h][i] = half8{};
+            }
+          } else {
+            const half8* src = reinterpret_cast<const half8*>(a.A + (size_t)arow[b][h] * a.lda + kc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[b][h][i] = aok[b][h] ? src[i] : half8{};
+          }
+        }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const __half2 s2 = __float2half2_rn(bsc[s]);
+        const uint32_t wd[4] = {braw[s].x ^ xor4, braw[s].y ^ xor4, braw[s].z ^ xor4, braw[s].w ^ xor4};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const half8 bv = widen8(wd[i], s2);
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
-            acc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.av[h][i], bv, acc[h][s], 0, 0, 0);
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              acc[b][h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[b][h][i], bv, acc[b][h][s], 0, 0, 0);
         }
       }
-    };
-    // operands are loaded right before use: holding the next step's operands in
-    // registers costs more occupancy (3 -> 2 or 1 waves per SIMD) than it
-    // hides latency
-    StepRegs r;
-    for (int st = wave; st < nsteps; st += 4) {
-      load_b(r, st);
-      load_a(r, st);
-      compute(r);
     }
-    // add the waves' partial tiles in wave order
+    // per row block: the waves' partial tiles added in wave order, then stored
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int b = 0; b < NB; ++b) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) red[((wave * 2 + h) * 4 + s) * 64 + lane] = acc[h][s];
-    __syncthreads();
-    // D layout: lane holds rows 4q .. 4q+3 of column ln of each 16x16 tile
-    auto sum_red = [&](int h, int s) {
-      f32x4 v = red[((0 * 2 + h) * 4 + s) * 64 + lane];
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int w = 1; w < 4; ++w) v += red[((w * 2 + h) * 4 + s) * 64 + lane];
-      return v;
-    };
-    if (MODE == MODE_GATE_UP) {
-      if (wave < 2) {
-        const int s = wave;
+        for (int s = 0; s < 2; ++s) red[((wave * 2 + h) * 2 + s) * 64 + lane] = acc[b][h][s];
+      __syncthreads();
+      // wave w finishes row half h = w & 1 of sub-tile pair / sub-tile (w >> 1)
+      const int h = wave & 1, s = wave >> 1;
+      auto sum_red = [&](int ss) {
+        f32x4 v = red[((0 * 2 + h) * 2 + ss) * 64 + lane];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const f32x4 g = sum_red(h, s), u = sum_red(h, s + 2);
+        for (int w = 1; w < 4; ++w) v += red[((w * 2 + h) * 2 + ss) * 64 + lane];
+        return v;
+      };
+      // D layout: lane holds rows 4q .. 4q+3 of column ln of each 16x16 tile
+      if (MODE == MODE_GATE_UP) {
+        if (s == 0) {
+          const f32x4 g = sum_red(0), u = sum_red(1);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int m = mb + 16 * h + 4 * q + j;
-            if (m < m1 && wok[s]) {
-              const int col = nbase + 16 * s + ln;
-              a.act[(size_t)m * a.ldact + perm_pos(col)] = (_Float16)(silu(g[j]) * u[j]);
-            }
+            const int m = mb + 32 * b + 16 * h + 4 * q + j;
+            if (m < m1 && wok[0]) a.act[(size_t)m * a.ldact + perm_pos(nbase + ln)] = (_Float16)(silu(g[j]) * u[j]);
           }
         }
-      }
-    } else {
-      const int s = wave;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const f32x4 v = sum_red(h, s);
+      } else {
+        const f32x4 v = sum_red(s);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int m = mb + 16 * h + 4 * q + j;
+          const int m = mb + 32 * b + 16 * h + 4 * q + j;
           if (m < m1 && wok[s]) a.Y[(size_t)m * a.ldy + nbase + 16 * s + ln] = v[j];
         }
       }
+      __syncthreads();  // red is reused by the next block / pass
     }
-    __syncthreads();  // the next row block reuses the LDS tiles
   }
 }
 
-template <int MODE, bool ROWS32>
+// NBMAX 2: an expert with more than 32 rows is done 64 rows per pass (its
+// weight tile read once for up to 64 rows); the others 32 rows per pass.
+template <int MODE, bool ROWS32, int NBMAX>
 __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
-  __shared__ f32x4 red[4 * 2 * 4 * 64];  // 32 KB: per wave, row half, sub-tile, lane
-  const int e = blockIdx.y;
+  __shared__ f32x4 red[4 * 2 * 2 * 64];  // 16 KB: per wave, row half, sub-tile, lane
+  // all column tiles of one expert on one XCD: its activation rows stay in that L2
+  const int L = xcd_contiguous(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+  const int e = L / gridDim.x, tile = L % gridDim.x;
   const int m0 = a.table ? a.eoff[e] : 0, m1 = a.table ? a.eoff[e + 1] : a.single_rows;
   if (m0 >= m1) return;
-  const int per_tile = MODE == MODE_GATE_UP ? 32 : 64;
-  const int nbase = blockIdx.x * per_tile;
+  const int per_tile = MODE == MODE_GATE_UP ? 16 : 32;
+  const int nbase = tile * per_tile;
   const ExpertDesc d = a.table ? a.table[e] : a.single;
   const uint8_t* Wt = a.which ? d.dn_w : d.gu_w;
   const void* S = a.which ? d.dn_s : d.gu_s;
   const uint32_t xor4 = d.xor8 * 0x01010101u;
-  if (d.s_f16) gemm_body<MODE, true, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, red);
-  else gemm_body<MODE, false, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, red);
+  if (NBMAX == 2 && m1 - m0 > 32) {
+    if (d.s_f16) gemm_body<MODE, true, ROWS32, 2>(a, Wt, S, xor4, m0, m1, nbase, red);
+    else gemm_body<MODE, false, ROWS32, 2>(a, Wt, S, xor4, m0, m1, nbase, red);
+  } else {
+    if (d.s_f16) gemm_body<MODE, true, ROWS32, 1>(a, Wt, S, xor4, m0, m1, nbase, red);
+    else gemm_body<MODE, false, ROWS32, 1>(a, Wt, S, xor4, m0, m1, nbase, red);
+  }
 }
 
 // ------------------------------------------------------------------ combine
@@ -524,20 +522,24 @@ int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Floa
   return check_launch("gather rows (f16)");
 }
 
-int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
+int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st, int rows_hint) {
   if (nexp <= 0) return MOE_OK;
-  const int per_tile = mode == MODE_GATE_UP ? 32 : 64;
+  const int per_tile = mode == MODE_GATE_UP ? 16 : 32;
   const int n = mode == MODE_GATE_UP ? a.I : a.N;
   dim3 grid((n + per_tile - 1) / per_tile, nexp);
+  // 64-row passes cost occupancy: only when some experts may hold > 32 rows
+  const bool two = rows_hint > 16;
   auto go = [&](auto k) { hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a); };
   if (a.rows32) {
-    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, true>);
-    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, true>);
+    if (mode == MODE_PLAIN) two ? go(gemm_q4_kernel<MODE_PLAIN, true, 2>) : go(gemm_q4_kernel<MODE_PLAIN, true, 1>);
+    else if (mode == MODE_GATE_UP)
+      two ? go(gemm_q4_kernel<MODE_GATE_UP, true, 2>) : go(gemm_q4_kernel<MODE_GATE_UP, true, 1>);
     else return set_error(MOE_EINVAL, "int4 grouped GEMM: the down product takes f16 activations");
   } else {
-    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, false>);
-    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, false>);
-    else go(gemm_q4_kernel<MODE_DOWN, false>);
+    if (mode == MODE_PLAIN) two ? go(gemm_q4_kernel<MODE_PLAIN, false, 2>) : go(gemm_q4_kernel<MODE_PLAIN, false, 1>);
+    else if (mode == MODE_GATE_UP)
+      two ? go(gemm_q4_kernel<MODE_GATE_UP, false, 2>) : go(gemm_q4_kernel<MODE_GATE_UP, false, 1>);
+    else two ? go(gemm_q4_kernel<MODE_DOWN, false, 2>) : go(gemm_q4_kernel<MODE_DOWN, false, 1>);
   }
   return check_launch("int4 grouped GEMM");
 }
