@@ -125,8 +125,8 @@ MOE_API int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* 
 
 MOE_API int moe_gguf_matmul_t(const float* x, int n, const uint8_t* raw, int qtype, int O, int cols, float* y,
                               void* stream) {
-  REQUIRE(qtype == FMT_Q8_0 || qtype == FMT_Q4_K, "moe_gguf_matmul_t: qtype %d (supported: 8 Q8_0, 12 Q4_K)",
-          qtype);
+  if (qtype != FMT_Q8_0 && qtype != FMT_Q4_K)
+    return set_error(MOE_EUNSUPPORTED, "moe_gguf_matmul_t: qtype %d (supported: 8 Q8_0, 12 Q4_K)", qtype);
   const int blk = qtype == FMT_Q8_0 ? 32 : 256;
   REQUIRE(O > 0 && cols > 0 && cols % blk == 0, "moe_gguf_matmul_t: cols=%d must be a positive multiple of %d",
           cols, blk);
@@ -163,7 +163,8 @@ MOE_API int moe_q8_dequant(const int8_t* q, const void* s, int s_f16, int O, int
 }
 
 MOE_API int moe_gguf_dequant(const uint8_t* raw, int qtype, int O, int cols, float* out, void* stream) {
-  REQUIRE(qtype == FMT_Q8_0 || qtype == FMT_Q4_K, "moe_gguf_dequant: qtype %d (supported: 8 Q8_0, 12 Q4_K)", qtype);
+  if (qtype != FMT_Q8_0 && qtype != FMT_Q4_K)
+    return set_error(MOE_EUNSUPPORTED, "moe_gguf_dequant: qtype %d (supported: 8 Q8_0, 12 Q4_K)", qtype);
   const int blk = qtype == FMT_Q8_0 ? 32 : 256;
   REQUIRE(O > 0 && cols > 0 && cols % blk == 0, "moe_gguf_dequant: cols=%d must be a positive multiple of %d", cols,
           blk);
@@ -358,10 +359,14 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   return run_gemm(MODE_DOWN, d, nexp, st, hint);
 }
 
+// shapes the MFMA tiles do not take are unsupported (not invalid for the format)
 static int check_mfma_shape(const char* who, int H, int I, int gs) {
-  REQUIRE(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0, "%s: H=%d and I=%d must be multiples of 128", who, H, I);
-  REQUIRE(gs > 0 && gs % 32 == 0 && H % gs == 0 && I % gs == 0,
-          "%s: group size %d must be a multiple of 32 dividing H=%d and I=%d", who, gs, H, I);
+  REQUIRE(H > 0 && I > 0 && gs > 0, "%s: H=%d, I=%d and gs=%d must be positive", who, H, I, gs);
+  if (H % 128 != 0 || I % 128 != 0)
+    return set_error(MOE_EUNSUPPORTED, "%s: H=%d and I=%d must be multiples of 128", who, H, I);
+  if (gs % 32 != 0 || H % gs != 0 || I % gs != 0)
+    return set_error(MOE_EUNSUPPORTED, "%s: group size %d must be a multiple of 32 dividing H=%d and I=%d", who, gs,
+                     H, I);
   return MOE_OK;
 }
 }  // namespace moe

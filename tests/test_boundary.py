@@ -68,6 +68,18 @@ def test_bad_arguments_fail_with_a_message(call, needle):
     assert needle in _lib.last_error()
 
 
+def test_unsupported_is_its_own_code():
+    """Formats and shapes the kernels do not take report MOE_EUNSUPPORTED, not MOE_EINVAL."""
+    L = _lib.lib()
+    assert L.moe_gguf_matmul_t(1, 1, 1, 14, 8, 256, 1, None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_gguf_dequant(1, 6, 8, 32, 1, None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_q4_grouped_ffn(1, 96, 1, 1, 1, 1, 4, 96, 128, 32, 1, 96, 1, 1 << 20, None) == _lib.MOE_EUNSUPPORTED
+    assert "multiples of 128" in _lib.last_error()
+    assert L.moe_q4_grouped_ffn(1, 128, 1, 1, 1, 1, 4, 128, 128, 16, 1, 128, 1, 1 << 20, None) == \
+        _lib.MOE_EUNSUPPORTED
+    assert L.moe_q4_grouped_ffn(1, 128, 1, 1, 1, 1, 4, -128, 128, 32, 1, 128, 1, 1 << 20, None) == _lib.MOE_EINVAL
+
+
 def test_empty_calls_are_no_ops():
     L = _lib.lib()
     assert L.moe_q4_matmul_t(None, 0, None, None, 0, 8, 64, 32, 0, None, None) == 0
