@@ -108,14 +108,14 @@ class Calls:
         parts, spec = [], []
         for eidx, rows, ws in calls:
             poff, prow, pw, rrow, rptr, rpair = kernels.pair_lists(rows, ws)
-            spec.append((len(eidx), int(poff[-1]), len(rrow), int(np.diff(poff).max())))
+            spec.append((len(eidx), int(poff[-1]), len(rrow), int(np.diff(poff).max()), int(np.diff(rptr).max())))
             parts += [np.asarray(eidx, np.int32).tobytes(), poff.tobytes(), prow.tobytes(), pw.tobytes(),
                       rrow.tobytes(), rptr.tobytes(), rpair.tobytes()]
         self.buf, addrs = kernels.upload_parts(parts)
-        for i, (k, P, nr, mr) in enumerate(spec):
+        for i, (k, P, nr, mr, mp) in enumerate(spec):
             a = addrs[7 * i:7 * i + 7]
             self.items.append(dict(eidx=a[0], poff=a[1], prow=a[2], pw=a[3], rrow=a[4], rptr=a[5], rpair=a[6],
-                                   k=k, P=P, nr=nr, max_rows=mr))
+                                   k=k, P=P, nr=nr, max_rows=mr, max_pairs=mp))
 
 
 def run_layer(L, pool, x, out, h, y, c, stream, ev=None):
@@ -132,8 +132,8 @@ def run_layer(L, pool, x, out, h, y, c, stream, ev=None):
                                   c["max_rows"], y.data_ptr(), H, stream)
     if ev is not None:
         ev[2].record()
-    rc |= L.moe_combine(y.data_ptr(), H, c["pw"], c["rrow"], c["rptr"], c["rpair"], c["nr"], out.data_ptr(), H, H,
-                        stream)
+    rc |= L.moe_combine(y.data_ptr(), H, c["pw"], c["rrow"], c["rptr"], c["rpair"], c["nr"], c["max_pairs"],
+                        out.data_ptr(), H, H, stream)
     if rc:
         from distributedmoellm_amd import _lib
         raise RuntimeError(_lib.last_error())

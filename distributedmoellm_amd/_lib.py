@@ -8,10 +8,12 @@ current HIP stream, so the kernels order with the caller's torch work.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_char_p, c_int, c_size_t, c_uint32, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).with_name("libmoehip.so")
+# MOEHIP_LIB names another build of the library (e.g. a tuning variant)
+LIB_PATH = Path(os.environ.get("MOEHIP_LIB") or Path(__file__).with_name("libmoehip.so"))
 
 MOE_OK, MOE_EINVAL, MOE_EHIP, MOE_EWORKSPACE, MOE_EUNSUPPORTED = 0, 1, 2, 3, 4
 
@@ -46,7 +48,7 @@ SIGNATURES = {
     "moe_q8_dequant": (c_int, [_P, _P, _I, _I, _I, _I, _P, _P]),
     "moe_gguf_dequant": (c_int, [_P, _I, _I, _I, _P, _P]),
     "moe_silu_mul": (c_int, [_P, _I, _I, _I, _P, _I, _P]),
-    "moe_combine": (c_int, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    "moe_combine": (c_int, [_P, _I, _P, _P, _P, _P, _I, _I, _P, _I, _I, _P]),
     "moe_q4_experts_matvec": (c_int, [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
     "moe_q4_layer_workspace": (c_size_t, [_I, _I, _I]),
     "moe_router_logits_workspace": (c_size_t, [_I, _I, _I]),

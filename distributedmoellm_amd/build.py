@@ -2,9 +2,10 @@
 
     python -m distributedmoellm_amd.build
 
-One hipcc invocation over csrc/*.hip. Packed-FP32 instruction selection is
-switched off (-packed-fp32-ops) on purpose; hipcc's host pass warns that it
-does not know the feature, which is harmless.
+Each csrc/*.hip is compiled to an object in a temporary directory, all at
+once (one hipcc process per source), then the objects are linked. Packed-FP32
+instruction selection is switched off (-packed-fp32-ops) on purpose; hipcc's
+host pass warns that it does not know the feature, which is harmless.
 """
 
 from __future__ import annotations
@@ -12,6 +13,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -21,7 +23,7 @@ LIB = PKG / "libmoehip.so"
 ARCH = os.environ.get("MOEHIP_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
@@ -38,18 +40,34 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+def _messages(r) -> list[str]:
+    return [ln for ln in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+
+
 def build(verbose: bool = True) -> Path:
     """Compile every source into libmoehip.so (always recompiles)."""
     srcs = sources()
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, *map(str, srcs), "-o", str(tmp)]
     t0 = time.time()
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    errors = [ln for ln in (r.stdout + r.stderr).splitlines()
-              if "packed-fp32-ops" not in ln and ln.strip()]
-    if r.returncode != 0:
-        sys.stderr.write("\n".join(errors) + "\n")
-        raise RuntimeError(f"hipcc failed ({r.returncode}) building {LIB.name}")
+    with tempfile.TemporaryDirectory(prefix="moehip-") as tmpdir:
+        objs = [Path(tmpdir) / (src.stem + ".o") for src in srcs]
+        procs = [subprocess.Popen([hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)],
+                                  stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+                 for src, obj in zip(srcs, objs)]
+        failed = []
+        for src, p in zip(srcs, procs):
+            out, err = p.communicate()
+            if p.returncode != 0:
+                failed.append(src.name)
+                sys.stderr.write("\n".join(_messages(subprocess.CompletedProcess(p.args, p.returncode, out, err)))
+                                 + "\n")
+        if failed:
+            raise RuntimeError(f"hipcc failed on {', '.join(failed)} building {LIB.name}")
+        tmp = LIB.with_suffix(".so.tmp")
+        r = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write("\n".join(_messages(r)) + "\n")
+            raise RuntimeError(f"linking {LIB.name} failed ({r.returncode})")
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources in {time.time() - t0:.1f}s")

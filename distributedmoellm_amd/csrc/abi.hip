@@ -226,12 +226,14 @@ MOE_API int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int ld
   return run_silu_mul(h, ldh, n, I, a, lda, as_stream(stream));
 }
 
-MOE_API int moe_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair,
-                        int nr, float* out, int ldo, int H, void* stream) {
-  REQUIRE(nr >= 0 && H > 0 && ldy >= H && ldo >= H, "moe_combine: nr=%d H=%d ldy=%d ldo=%d", nr, H, ldy, ldo);
+MOE_API int moe_combine(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
+                        int max_pairs, float* out, int ldo, int H, void* stream) {
+  REQUIRE(nr >= 0 && H > 0 && ldy >= H && ldo >= H && max_pairs >= 0,
+          "moe_combine: nr=%d H=%d ldy=%d ldo=%d max_pairs=%d", nr, H, ldy, ldo, max_pairs);
   if (nr == 0) return MOE_OK;
   REQUIRE(y && pw && rrow && rptr && rpair && out, "moe_combine: null pointer");
-  return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, as_stream(stream));
+  if (max_pairs == 0) return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, as_stream(stream));
+  return run_combine_runs(y, ldy, pw, rrow, rptr, rpair, nr, max_pairs, out, ldo, H, as_stream(stream));
 }
 
 MOE_API int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4_expert* table,

@@ -72,7 +72,8 @@ __device__ __forceinline__ float gguf_half(uint32_t h) {
   return half_bits_to_float(h);
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+// g / (1 + e^-g) with the hardware exp and reciprocal (a few ulp; no IEEE divide)
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // sum over aligned groups of `width` lanes (width a power of two <= 64)
 __device__ __forceinline__ float group_sum(float v, int width) {

@@ -2,8 +2,9 @@
 // (moelan/kernels.py:712-782, _moe_q4; wrapper 942-968):
 //   1. gate|up of every (expert, row) pair      h[p]  = x[prow[p]] @ GU_e.T
 //   2. down of silu(gate)*up, fused on load     y[p]  = a(h[p]) @ DN_e.T
-//   3. weighted sum per touched row, in pair order (expert order), then
-//      added to out:  out[r] += sum_p pw[p] * y[p]      (deterministic)
+//   3. weighted sum per touched row, in runs of 8 pairs in pair order
+//      (expert order), then added to out: out[r] += sum_p pw[p] * y[p]
+//      (deterministic)
 #include "common.h"
 #include "matvec.h"
 #include "layer.h"
@@ -71,6 +72,111 @@ int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const
   return check_launch("weighted combine");
 }
 
+// The layer call's combine, in two launches, for rows with many pairs (one
+// token's 384 experts): the pair list of a row is cut into runs of kRun pairs
+// in list order. Launch 1: a block sums one run for 1024 columns (a thread
+// takes 4 columns, its kRun loads issued together) and writes the partial sum
+// over the y row of the run's first pair, which no other block reads (each
+// pair belongs to one row and one run); a row with a single run is added to
+// out at once. Launch 2: per row of more than one run, the partial sums in
+// run order, added to out. Fixed order, no atomics. y is overwritten.
+constexpr int kRun = 8;
+
+__global__ __launch_bounds__(256) void combine_runs_kernel(float* y, int ldy, const float* pw, const int* rrow,
+                                                           const int* rptr, const int* rpair, int nr, float* out,
+                                                           int ldo, int H) {
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= H) return;
+  for (int i = blockIdx.y; i < nr; i += gridDim.y) {
+    const int r0 = rptr[i], r1 = rptr[i + 1];
+    for (int q0 = r0 + blockIdx.z * kRun; q0 < r1; q0 += gridDim.z * kRun) {
+      const int n = min(kRun, r1 - q0);
+      int ps[kRun];
+      float ws[kRun];
+      float4 v[kRun];
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        ps[j] = rpair[q0 + (j < n ? j : 0)];
+        ws[j] = j < n ? pw[ps[j]] : 0.f;
+        v[j] = *reinterpret_cast<const float4*>(y + (size_t)ps[j] * ldy + c);
+      }
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        if (j < n) {
+          a.x += ws[j] * v[j].x;
+          a.y += ws[j] * v[j].y;
+          a.z += ws[j] * v[j].z;
+          a.w += ws[j] * v[j].w;
+        }
+      }
+      if (r1 - r0 <= kRun) {
+        float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+        float4 o = *dst;
+        o.x += a.x;
+        o.y += a.y;
+        o.z += a.z;
+        o.w += a.w;
+        *dst = o;
+      } else {
+        *reinterpret_cast<float4*>(y + (size_t)ps[0] * ldy + c) = a;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void combine_partials_kernel(const float* y, int ldy, const int* rrow,
+                                                               const int* rptr, const int* rpair, int nr, float* out,
+                                                               int ldo, int H) {
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= H) return;
+  for (int i = blockIdx.y; i < nr; i += gridDim.y) {
+    const int r0 = rptr[i], r1 = rptr[i + 1];
+    if (r1 - r0 <= kRun) continue;
+    const int runs = (r1 - r0 + kRun - 1) / kRun;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < runs; s0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int s = s0 + j < runs ? s0 + j : s0;
+        v[j] = *reinterpret_cast<const float4*>(y + (size_t)rpair[r0 + s * kRun] * ldy + c);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < runs) {
+          a.x += v[j].x;
+          a.y += v[j].y;
+          a.z += v[j].z;
+          a.w += v[j].w;
+        }
+      }
+    }
+    float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+    float4 o = *dst;
+    o.x += a.x;
+    o.y += a.y;
+    o.z += a.z;
+    o.w += a.w;
+    *dst = o;
+  }
+}
+
+// max_pairs: an upper bound of the pairs of one row
+int run_combine_runs(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair,
+                            int nr, int max_pairs, float* out, int ldo, int H, hipStream_t st) {
+  if (nr <= 0) return MOE_OK;
+  const bool vec4 = H % 4 == 0 && ldy % 4 == 0 && ldo % 4 == 0 && aligned(y, 16) && aligned(out, 16);
+  if (!vec4) return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, st);
+  const int runs = (max_pairs + kRun - 1) / kRun;
+  const dim3 grid((H + 1023) / 1024, nr < 65535 ? nr : 65535, runs < 1 ? 1 : (runs < 1024 ? runs : 1024));
+  hipLaunchKernelGGL(combine_runs_kernel, grid, dim3(256), 0, st, y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H);
+  if (runs > 1)
+    hipLaunchKernelGGL(combine_partials_kernel, dim3(grid.x, grid.y), dim3(256), 0, st, y, ldy, rrow, rptr, rpair, nr,
+                       out, ldo, H);
+  return check_launch("weighted combine");
+}
+
 size_t q4_layer_workspace(int P, int H, int I) { return (size_t)P * (2 * (size_t)I + H) * sizeof(float); }
 
 int run_q4_layer(const Q4LayerArgs& a, hipStream_t st) {
@@ -108,7 +214,8 @@ int run_q4_layer(const Q4LayerArgs& a, hipStream_t st) {
   rc = run_matvec(FMT_Q4, s2, j2, a.k, a.max_rows, st);
   if (rc) return rc;
 
-  return run_combine(y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.out, a.ldo, a.H, st);
+  // a row has at most one pair per expert of the call
+  return run_combine_runs(y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st);
 }
 
 }  // namespace moe

@@ -221,13 +221,14 @@ __device__ __forceinline__ float dpp_read(float v) {
 }
 
 // lane L-1 of every aligned group of L lanes receives the group's sum
-__device__ __forceinline__ float lane_group_sum(float v, int L) {
+template <int L>
+__device__ __forceinline__ float lane_group_sum(float v) {
   v += dpp_read<0x111, 0xf, true>(v);  // row_shr:1
   v += dpp_read<0x112, 0xf, true>(v);  // row_shr:2
   v += dpp_read<0x114, 0xf, true>(v);  // row_shr:4
-  if (L >= 16) v += dpp_read<0x118, 0xf, true>(v);   // row_shr:8
-  if (L >= 32) v += dpp_read<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1, 3
-  if (L >= 64) v += dpp_read<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2, 3
+  if constexpr (L >= 16) v += dpp_read<0x118, 0xf, true>(v);   // row_shr:8
+  if constexpr (L >= 32) v += dpp_read<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1, 3
+  if constexpr (L >= 64) v += dpp_read<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2, 3
   return v;
 }
 
@@ -252,20 +253,43 @@ __device__ __forceinline__ uint4 wload16(const uint8_t* p) {
   }
 }
 
+// a scale's bits; converted when used, so that its load is not waited for early
 template <bool SF16>
-__device__ __forceinline__ float sload(const void* s, size_t idx) {
-  if constexpr (SF16) return half_bits_to_float(gptr<uint16_t>(s)[idx]);
-  else return gptr<float>(s)[idx];
+__device__ __forceinline__ uint32_t sload_bits(const void* s, uint32_t idx) {
+  if constexpr (SF16) return gptr<uint16_t>(s)[idx];
+  else return gptr<uint32_t>(s)[idx];
 }
 
-template <class F, int CPL, int NR, bool SF16, bool A16>
-__device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job, const MatRef& M, int L, int A,
-                                             int ng, int p0, int p1, int row_begin) {
+template <bool SF16>
+__device__ __forceinline__ float scale_value(uint32_t bits) {
+  if constexpr (SF16) return half_bits_to_float(bits);
+  else return __builtin_bit_cast(float, bits);
+}
+
+// Lane (lg, lc) of a wave works on row lg of each pass of 64/L rows, chunks
+// lc, lc + A, ... of it (A <= L lanes of a group are active). Everything a
+// lane needs per row is a 24-bit multiply from a uniform base: the chunk
+// offsets and scale indices are fixed per lane. Rows past the end of the
+// matrix are read as its last row (in bounds) and not stored.
+template <class F, int L, int CPL, int NR, bool SF16, bool A16>
+__device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job, const MatRef& M, int A, int ng,
+                                             int p0, int p1, int row_begin) {
   constexpr int G = fast_group<CPL, NR>();
+  constexpr int RPP = 64 / L;
   const int lane = threadIdx.x & 63;
-  const int rpp = 64 / L, lg = lane / L, lc = lane % L;
+  const int lg = lane / L, lc = lane % L;
   const bool active = lc < A;  // the first A lanes of a group own the row's chunks
   const int gdiv = sh.gs / F::VALS;  // chunks per scale group (gs is a multiple of VALS here)
+  uint32_t woff[CPL], soff[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int chunk = active ? lc + c * A : 0;
+    woff[c] = (uint32_t)chunk * 16u;
+    soff[c] = (uint32_t)(chunk / gdiv);
+  }
+  const uint32_t omax = (uint32_t)sh.O - 1u, rb = (uint32_t)sh.row_bytes, gpr = (uint32_t)sh.G;
+  const uint8_t* const W = M.w;
+  const void* const S = M.s;
 
   for (int pb = p0; pb < p1; pb += NR) {
     float xr[NR][CPL][F::XR];
@@ -291,31 +315,25 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
     }
 
     uint4 wb[2][G][CPL];
-    float sb[2][G][CPL];
+    uint32_t sb[2][G][CPL];
     // buffers are named by compile-time constants only, so they stay in VGPRs
     auto issue = [&](auto buf, int grp) {
       constexpr int B = decltype(buf)::value;
-      const int rbase = row_begin + grp * G * rpp + lg;
+      const uint32_t obase = (uint32_t)(row_begin + grp * (G * RPP) + lg);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const int o = rbase + g * rpp;
-        const bool on = o < sh.O && grp < ng && active;
+        const uint32_t o = min(obase + (uint32_t)(g * RPP), omax);
+        const uint32_t wrow = __umul24(o, rb), srow = __umul24(o, gpr);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-          const int chunk = lc + c * A;
-          // rows past the end read row 0 (in bounds) and are dropped below
-          const int oo = on ? o : 0;
-          const int cc = on ? chunk : 0;
-          // unconditional loads (always in bounds): no branch, so no wait between them
-          wb[B][g][c] = wload16<A16>(M.w + (size_t)oo * sh.row_bytes + (size_t)cc * 16);
-          const float sv = sload<SF16>(M.s, (size_t)oo * sh.G + cc / gdiv);
-          sb[B][g][c] = on ? sv : 0.f;
+          wb[B][g][c] = wload16<A16>(W + (wrow + woff[c]));
+          sb[B][g][c] = sload_bits<SF16>(S, srow + soff[c]);
         }
       }
     };
     auto compute = [&](auto buf, int grp) {
       constexpr int B = decltype(buf)::value;
-      const int rbase = row_begin + grp * G * rpp + lg;
+      const int obase = row_begin + grp * (G * RPP) + lg;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float acc[NR];
@@ -323,10 +341,11 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
         for (int r = 0; r < NR; ++r) {
           float a = 0.f;
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) a = fmaf(F::dot(wb[B][g][c], M.xor4, xr[r][c]), sb[B][g][c], a);
-          acc[r] = lane_group_sum(a, L);
+          for (int c = 0; c < CPL; ++c)
+            a = fmaf(F::dot(wb[B][g][c], M.xor4, xr[r][c]), scale_value<SF16>(sb[B][g][c]), a);
+          acc[r] = lane_group_sum<L>(a);
         }
-        const int o = rbase + g * rpp;
+        const int o = obase + g * RPP;
         if (lc == L - 1 && o < sh.O) {
 #pragma unroll
           for (int r = 0; r < NR; ++r)
@@ -336,14 +355,23 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
+    // steady state with unconditional issues (the compiler's wait counts then
+    // leave one buffer in flight while the other is used), then the last one
+    // or two groups
     issue(B0{}, 0);
-    for (int grp = 0; grp < ng; grp += 2) {
+    int grp = 0;
+    for (; grp + 2 < ng; grp += 2) {
       issue(B1{}, grp + 1);
       compute(B0{}, grp);
-      if (grp + 1 < ng) {
-        issue(B0{}, grp + 2);
-        compute(B1{}, grp + 1);
-      }
+      issue(B0{}, grp + 2);
+      compute(B1{}, grp + 1);
+    }
+    if (grp + 1 < ng) {
+      issue(B1{}, grp + 1);
+      compute(B0{}, grp);
+      compute(B1{}, grp + 1);
+    } else {
+      compute(B0{}, grp);
     }
   }
 }
@@ -351,8 +379,8 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
 // One launch covers every matrix of the call (grid.y); the scale type and the
 // weight alignment are uniform per matrix, so the specialised body is chosen
 // once at the top.
-template <class F, int CPL, int NR>
-__global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int L, int A, int ng) {
+template <class F, int L, int CPL, int NR>
+__global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int A, int ng) {
   constexpr int G = fast_group<CPL, NR>();
   const int mat = blockIdx.y;
   int p0 = 0, p1 = job.n;
@@ -368,11 +396,11 @@ __global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int
   const MatRef M = resolve(job, mat);
   const bool a16 = aligned(M.w, 16);
   if (M.s_f16) {
-    if (a16) mv_fast_body<F, CPL, NR, true, true>(sh, job, M, L, A, ng, p0, p1, row_begin);
-    else mv_fast_body<F, CPL, NR, true, false>(sh, job, M, L, A, ng, p0, p1, row_begin);
+    if (a16) mv_fast_body<F, L, CPL, NR, true, true>(sh, job, M, A, ng, p0, p1, row_begin);
+    else mv_fast_body<F, L, CPL, NR, true, false>(sh, job, M, A, ng, p0, p1, row_begin);
   } else {
-    if (a16) mv_fast_body<F, CPL, NR, false, true>(sh, job, M, L, A, ng, p0, p1, row_begin);
-    else mv_fast_body<F, CPL, NR, false, false>(sh, job, M, L, A, ng, p0, p1, row_begin);
+    if (a16) mv_fast_body<F, L, CPL, NR, false, true>(sh, job, M, A, ng, p0, p1, row_begin);
+    else mv_fast_body<F, L, CPL, NR, false, false>(sh, job, M, A, ng, p0, p1, row_begin);
   }
 }
 
@@ -513,23 +541,30 @@ static void launch_fmt(const MVShape& sh, const MVJob& job, int nmat, int max_ro
   else launch_nr<F, 4, P>(sh, job, nmat, st);
 }
 
-template <class F, int CPL>
-static void launch_fast_cpl(const MVShape& sh, const MVJob& job, int nmat, int nr, int L, int A, hipStream_t st) {
+template <class F, int L, int CPL>
+static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr, int A, hipStream_t st) {
   auto go = [&](auto kernel, int G) {
-    const int rpp = 64 / L;
+    constexpr int rpp = 64 / L;
     const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));  // wave groups in the launch
     // runs of several groups per wave amortise the activation set-up; keep
     // at least ~8 waves per CU of the 256 in flight
+    // (longer runs when the activations are SiLU(gate) * up, computed per wave)
+    static const int ng_env = [] {
+      const char* e = getenv("MOEHIP_MV_NGMAX");  // tuning override
+      const int v = e ? atoi(e) : 0;
+      return v >= 1 && v <= 64 ? v : 0;
+    }();
+    const int ng_max = ng_env ? ng_env : (job.half_in > 0 ? 32 : 8);
     int ng = (int)(groups / 2048);
-    ng = ng < 1 ? 1 : (ng > 8 ? 8 : ng);
+    ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
     const int wave_rows = ng * G * rpp;
     const int waves = (sh.O + wave_rows - 1) / wave_rows;
     dim3 grid((waves + 3) / 4, nmat);
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, sh, job, L, A, ng);
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, sh, job, A, ng);
   };
-  if (nr == 1) go(mv_fast_kernel<F, CPL, 1>, fast_group<CPL, 1>());
-  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, CPL, 2>, fast_group<CPL, 2>());
-  else go(mv_fast_kernel<F, 1, 4>, fast_group<1, 4>());
+  if (nr == 1) go(mv_fast_kernel<F, L, CPL, 1>, fast_group<CPL, 1>());
+  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, L, CPL, 2>, fast_group<CPL, 2>());
+  else go(mv_fast_kernel<F, L, 1, 4>, fast_group<1, 4>());
 }
 
 // Lanes per row: by default one chunk per lane whenever a row has at most 64
@@ -558,19 +593,26 @@ static void lanes_for(int cpr, int* L, int* A, int* cpl) {
   *cpl = cpr / l;
 }
 
+// false: the shape goes to the general kernels
 template <class F>
 static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   if (sh.cpr % 8 != 0) return false;
   int L, A, cpl;
   lanes_for(sh.cpr, &L, &A, &cpl);
-  if (L < 8 || cpl > 4) return false;
   const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
-  switch (cpl) {
-    case 1: launch_fast_cpl<F, 1>(sh, job, nmat, nr, L, A, st); return true;
-    case 2: launch_fast_cpl<F, 2>(sh, job, nmat, nr, L, A, st); return true;
-    case 3: launch_fast_cpl<F, 3>(sh, job, nmat, nr, L, A, st); return true;
-    case 4: launch_fast_cpl<F, 4>(sh, job, nmat, nr, L, A, st); return true;
+  if (L == 64) {
+    switch (cpl) {
+      case 1: launch_fast_l<F, 64, 1>(sh, job, nmat, nr, A, st); return true;
+      case 2: launch_fast_l<F, 64, 2>(sh, job, nmat, nr, A, st); return true;
+      case 3: launch_fast_l<F, 64, 3>(sh, job, nmat, nr, A, st); return true;
+      case 4: launch_fast_l<F, 64, 4>(sh, job, nmat, nr, A, st); return true;
+    }
+    return false;
   }
+  if (L == 32 && cpl == 1) { launch_fast_l<F, 32, 1>(sh, job, nmat, nr, A, st); return true; }
+  if (L == 32 && cpl == 2) { launch_fast_l<F, 32, 2>(sh, job, nmat, nr, A, st); return true; }
+  if (L == 16 && cpl == 1) { launch_fast_l<F, 16, 1>(sh, job, nmat, nr, A, st); return true; }
+  if (L == 8 && cpl == 1) { launch_fast_l<F, 8, 1>(sh, job, nmat, nr, A, st); return true; }
   return false;
 }
 

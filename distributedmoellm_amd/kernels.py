@@ -299,8 +299,10 @@ def combine(out, ys, rows, weights) -> None:
     _, _, pw, rrow, rptr, rpair = pair_lists(rows, weights)
     buf, (pw_p, rrow_p, rptr_p, rpair_p) = upload_parts([pw.tobytes(), rrow.tobytes(), rptr.tobytes(),
                                                          rpair.tobytes()])
-    _lib.call("moe_combine", _ptr(y), H, pw_p, rrow_p, rptr_p, rpair_p, len(rrow), _ptr(out), out.shape[1], H,
-              stream_handle())
+    # y is a temporary here: the kernel may use it as scratch
+    max_pairs = int(np.diff(rptr).max())
+    _lib.call("moe_combine", _ptr(y), H, pw_p, rrow_p, rptr_p, rpair_p, len(rrow), max_pairs, _ptr(out),
+              out.shape[1], H, stream_handle())
 
 
 class LayerMeta:

@@ -93,11 +93,14 @@ int moe_gguf_dequant(const uint8_t* raw, int qtype, int O, int cols, float* out,
 int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, void* stream);
 
 /* out[rrow[i]] += sum over q in rptr[i]..rptr[i+1] of pw[p] * y[p], p = rpair[q],
- * the sum formed in that order first: the weighted combine of per-expert
- * outputs, out[rows] += e(x[rows]) * w, moelan/experts.py:648-651, 707-727
- * and moelan/kernels.py:778-782, 968. y [P, H] (stride ldy), out stride ldo. */
-int moe_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
-                float* out, int ldo, int H, void* stream);
+ * summed in that order in runs of 8 pairs (the runs' sums then added in run
+ * order) and then added to out: the weighted combine of per-expert outputs,
+ * out[rows] += e(x[rows]) * w, moelan/experts.py:648-651, 707-727 and
+ * moelan/kernels.py:778-782, 968. y [P, H] (stride ldy) is also scratch: its
+ * contents are overwritten. max_pairs bounds the pairs of one row (0: not
+ * known; one workgroup then sums a whole row). out stride ldo. */
+int moe_combine(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
+                int max_pairs, float* out, int ldo, int H, void* stream);
 
 /* -------------------------------------------- one MoE layer, few rows each */
 
@@ -119,7 +122,8 @@ size_t moe_q4_layer_workspace(int P, int H, int I);
  * given as table[eidx[m]] (eidx NULL: table[m]) with pairs poff[m]..poff[m+1]
  * (input rows prow[p], gate weights pw[p]). Rows touched: rrow[0..nr), whose
  * pairs are rpair[rptr[i]..rptr[i+1]] in ascending order; each row's sum is
- * formed in that order and then added to out, as the reference does.
+ * formed in that order (in runs of 8 pairs, the runs' sums added in run
+ * order) and then added to out, as the reference does.
  * max_rows: the largest poff[m+1]-poff[m]. All arrays: device.
  * Replaces moe_q4(x, items, H, I, gs, out), moelan/kernels.py:942-968
  * (_moe_q4 :712-782, float activations). */

@@ -59,7 +59,8 @@ def test_struct_layout():
                               1, 10, None), "workspace"),
     (lambda L: L.moe_q4_layer(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 24, 1,
                               1, 10, None), "group size 24"),
-    (lambda L: L.moe_combine(1, 8, 1, 1, 1, 1, 1, 1, 8, 16, None), "ldy=8"),
+    (lambda L: L.moe_combine(1, 8, 1, 1, 1, 1, 1, 0, 1, 8, 16, None), "ldy=8"),
+    (lambda L: L.moe_combine(1, 16, 1, 1, 1, 1, 1, -1, 1, 16, 16, None), "max_pairs=-1"),
 ])
 def test_bad_arguments_fail_with_a_message(call, needle):
     L = _lib.lib()

@@ -113,6 +113,35 @@ def test_qwen3_30b_layer_decode(kernels, rows_per_token, k):
     close(out, R.moe_q4(x, oitems, np.zeros(x.shape)))
 
 
+@pytest.mark.parametrize("k,counts", [(384, (384,)), (100, (100, 21, 8, 9, 1))])
+def test_rows_with_many_pairs(kernels, k, counts):
+    """A row in many experts' pair lists (one token's 48 layers x top-8 in one
+    call): the weighted sum over runs of pairs, added into a non-zero out."""
+    rng = np.random.default_rng(k)
+    H, I = 256, 128
+    experts = [X.synthetic_expert(H, I, "int4", 32, rng) for _ in range(k)]
+    T = len(counts)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    member = np.zeros((k, T), bool)
+    for t, c in enumerate(counts):
+        member[rng.choice(k, size=c, replace=False), t] = True
+    items, oitems = [], []
+    for i, e in enumerate(experts):
+        rows = np.nonzero(member[i])[0].astype(np.int32)
+        if len(rows) == 0:
+            continue
+        w = rng.random(len(rows)).astype(np.float32)
+        items.append((kernels.q4_expert_ptrs(e), rows, w))
+        oitems.append((lambda xr, e=e: R.expert_exact(xr, *oracle_expert(e)), rows, w))
+    delta = R.moe_q4(x, oitems, np.zeros((T, H)))
+    # out starts at values of the size of what is added, so 1e-5 measures the sum
+    base = (rng.standard_normal((T, H)) * delta.std()).astype(np.float32)
+    out = base.copy()
+    kernels.moe_q4(x, items, H, I, 32, out)
+    close(out, base + delta)
+    close(out - base, delta, rtol=1e-4)
+
+
 def test_expert_call_int4_int8_gguf(kernels):
     """Expert.__call__ for each format against the oracle's SwiGLU."""
     rng = np.random.default_rng(3)
