@@ -344,8 +344,7 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   g.gs = gs;
   g.act = act;
   g.ldact = I;
-  const int hint = nexp > 0 ? (P + nexp - 1) / nexp : P;
-  int rc = run_gemm(MODE_GATE_UP, g, nexp, st, hint);
+  int rc = run_gemm(MODE_GATE_UP, g, nexp, st);
   if (rc) return rc;
   GemmArgs d{};
   d.A = act;
@@ -358,7 +357,7 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   d.gs = gs;
   d.Y = y;
   d.ldy = ldy;
-  return run_gemm(MODE_DOWN, d, nexp, st, hint);
+  return run_gemm(MODE_DOWN, d, nexp, st);
 }
 
 // shapes the MFMA tiles do not take are unsupported (not invalid for the format)
@@ -490,5 +489,5 @@ MOE_API int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s
   g.gs = gs;
   g.Y = y;
   g.ldy = O;
-  return run_gemm(MODE_PLAIN, g, 1, as_stream(stream), n);
+  return run_gemm(MODE_PLAIN, g, 1, as_stream(stream));
 }

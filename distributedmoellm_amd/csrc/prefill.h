@@ -39,8 +39,7 @@ size_t group_lds_bytes(int T, int E);
 int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
               int* experts, int* offsets, int* n_used, hipStream_t st);
 int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, hipStream_t st);
-// rows_hint: typical rows per expert (picks one or two 32-row blocks per pass)
-int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st, int rows_hint);
+int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st);
 int run_token_combine(const float* y, int ldy, const int* pos, const float* wts, int T, int k, int H, float* out,
                       int ldo, hipStream_t st);
 

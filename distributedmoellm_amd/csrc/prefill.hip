@@ -23,6 +23,8 @@
 #include "matvec.h"
 #include "prefill.h"
 
+#include <type_traits>
+
 namespace moe {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -258,176 +260,243 @@ __device__ __forceinline__ half8 widen8(uint32_t w, __half2 s2) {
   return out;
 }
 
+// A workgroup computes the output tile of one expert for up to 64 of its rows
+// (4 row tiles of 16) and 128 weight rows: wave w owns weight rows 32w ..
+// 32w+31 of the tile as two 16-row sub-tiles.
+//   MODE_PLAIN / MODE_DOWN: sub-tile s = weight rows n0 + 32w + 16s ..; y f32
+//   MODE_GATE_UP: sub-tile 0 = gate rows j0 + 16w .., 1 = the up rows I + j0 +
+//                 16w ..; act = silu(gate) * up as f16, columns in MFMA order
+// K advances in steps of 128. The step's activation tile (64 rows x 128
+// f16 = 16 KB) is staged in LDS once and read by all four waves (double
+// buffered, one barrier per step; wave w loads rows 16w .. 16w+15). Each
+// lane streams 16 bytes (32 nibbles) of each of its two weight rows per step,
+// issued one step ahead, widens them to f16 with the group scale once and
+// feeds them to every row tile: 2 x 4 x RT MFMAs per step. Rows of a pass past
+// the expert's last row repeat its last row and are not stored. An expert
+// with more than 64 rows is done in passes (its weight tile read again).
+// Activations: f16 rows (8-column groups in MFMA order), or f32 rows of X
+// gathered through `rows` and rounded to f16 when staged.
+
+constexpr int kGK = 128;                   // K per step
+constexpr int kGRows = 64;                 // expert rows per pass
+constexpr int kARow = kGK * 2 + 16;        // LDS bytes per activation row (16 B of padding: conflict-free)
+constexpr int kABuf = kGRows * kARow;      // one step's activation tile
+
 template <bool SF16>
-__device__ __forceinline__ float gscale(const void* s, size_t i) {
-  if constexpr (SF16) return half_bits_to_float(gptr<uint16_t>(s)[i]);
-  else return gptr<float>(s)[i];
+__device__ __forceinline__ uint32_t gscale_bits(const void* s, uint32_t i) {
+  if constexpr (SF16) return gptr<uint16_t>(s)[i];
+  else return gptr<uint32_t>(s)[i];
 }
 
-// A workgroup computes an output tile of one expert: up to 64 of its rows
-// (NB = 1 or 2 blocks of 32 = 2 x 16) against 32 weight rows (2 sub-tiles of
-// 16); its 4 waves split K: wave w takes the 128-wide K steps w, w+4, ...,
-// and the partial tiles are added through LDS in wave order at the end
-// (deterministic). There is no barrier in the K loop. Per step a lane reads
-// 16 bytes (32 nibbles) of each of its 2 weight rows, widens them to f16 with
-// the group scale once, and uses them for every row block: 2 x 4 x NB x 2
-// MFMAs. An expert with more rows than one pass holds is done in passes
-// (its weight tile is then read again, from L2).
-//   MODE_PLAIN / MODE_DOWN: sub-tile s = weight rows n0 + 16 s .. ; y f32
-//   MODE_GATE_UP: sub-tile 0 = gate rows j0 .. j0+15, 1 = up rows I + j0 ..;
-//                 act = silu(gate) * up as f16, columns in MFMA order
-// Activations: f16 rows (8-column groups in MFMA order), or f32 rows of X
-// gathered through `rows` and rounded to f16 on load.
+template <bool SF16>
+__device__ __forceinline__ float gscale_value(uint32_t bits) {
+  if constexpr (SF16) return half_bits_to_float(bits);
+  else return __builtin_bit_cast(float, bits);
+}
 
-template <int MODE, bool SF16, bool ROWS32, int NB>
-__device__ __forceinline__ void gemm_body(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
-                                          int m1, int nbase, f32x4* red) {
+struct WeightStep {
+  uint4 w[2];      // 16 bytes of each sub-tile row
+  uint32_t s[2];   // their group scales' bits
+};
+
+template <int MODE, bool SF16, bool ROWS32>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
+                                          int m1, int nbase, uint8_t* lds) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, q = lane >> 4;
-  const int row_bytes = a.K / 2, G = a.K / a.gs;
-  int wrow[2];
+  const uint32_t row_bytes = (uint32_t)a.K / 2, G = (uint32_t)(a.K / a.gs);
+  const int nsteps = a.K / kGK;
+  uint32_t wrow[2];
   bool wok[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (MODE == MODE_GATE_UP) {
-      const int j = nbase + ln;
+      const int j = nbase + 16 * wave + ln;
       wok[s] = j < a.I;
-      wrow[s] = (s == 0 ? 0 : a.I) + (wok[s] ? j : 0);
+      wrow[s] = (s == 0 ? 0u : (uint32_t)a.I) + (uint32_t)(wok[s] ? j : 0);
     } else {
-      const int n = nbase + 16 * s + ln;
+      const int n = nbase + 32 * wave + 16 * s + ln;
       wok[s] = n < a.N;
-      wrow[s] = wok[s] ? n : 0;
+      wrow[s] = (uint32_t)(wok[s] ? n : 0);
     }
   }
-  const int nsteps = a.K / 128;
-  constexpr int RB = 32 * NB;  // rows per pass
+  // the lane's 32-column run of step st starts at column 128 st + 32 q; its
+  // group is (4 st + q) / (gs / 32): a step advances it by 4 / (gs / 32) when
+  // that divides, else it is divided out per step
+  const int g32 = a.gs / 32;
+  const bool g_div = 4 % g32 == 0;
+  const uint32_t g_step = g_div ? (uint32_t)(4 / g32) : 0u;
+  const uint32_t wofs[2] = {wrow[0] * row_bytes + 16u * q, wrow[1] * row_bytes + 16u * q};
+  const uint32_t sofs[2] = {wrow[0] * G + (g_div ? (uint32_t)(q / g32) : 0u),
+                            wrow[1] * G + (g_div ? (uint32_t)(q / g32) : 0u)};
+  auto load_w = [&](int st, WeightStep& b) {
+    const uint32_t grp = g_div ? (uint32_t)st * g_step : (uint32_t)((4 * st + q) / g32);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      b.w[s] = stream_load16(Wt + (wofs[s] + (uint32_t)st * (kGK / 2)));
+      b.s[s] = gscale_bits<SF16>(S, sofs[s] + grp);
+    }
+  };
 
-  for (int mb = m0; mb < m1; mb += RB) {
-    int arow[NB][2];
-    bool aok[NB][2];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int m = mb + 32 * b + 16 * h + ln;
-        aok[b][h] = m < m1;
-        const int mm = aok[b][h] ? m : m0;
-        arow[b][h] = ROWS32 ? (a.rows ? a.rows[mm] : mm) : mm;
-      }
-    f32x4 acc[NB][2][2];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) acc[b][h][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // staging: lane (row 16 wave + lane / 4, 64-byte segment lane % 4) of the tile
+  const int lrow = 16 * wave + (lane >> 2), lseg = lane & 3;
+  uint8_t* const lds_dst = lds + lrow * kARow + lseg * 64;
 
-    for (int st = wave; st < nsteps; st += 4) {
-      const int kc = st * 128 + 32 * q;  // this lane's 32-column run
-      uint4 braw[2];
-      float bsc[2];
+  for (int mb = m0; mb < m1; mb += kGRows) {
+    const int rows = min(kGRows, m1 - mb), RT = (rows + 15) >> 4;
+    const int am = mb + min(lrow, rows - 1);
+    const int arow = ROWS32 ? (a.rows ? a.rows[am] : am) : am;
+    // a step's slice of this lane's activation row: 64 bytes of f16 (4 x uint4),
+    // or 32 floats (8 x float4); two sets, named by compile-time constants only
+    // (so that they stay in registers)
+    using AVec = std::conditional_t<ROWS32, float4, u32x4>;
+    constexpr int kAV = ROWS32 ? 8 : 4;
+    AVec areg[2][kAV];
+    auto load_a = [&](int st, auto set) {
+      constexpr int R = decltype(set)::value;
+      const AVec* src = reinterpret_cast<const AVec*>(ROWS32 ? (const void*)(a.X + (size_t)arow * a.ldx + st * kGK + 32 * lseg)
+                                                             : (const void*)(a.A + (size_t)arow * a.lda + st * kGK + 32 * lseg));
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        braw[s] = stream_load16(Wt + (size_t)wrow[s] * row_bytes + kc / 2);
-        bsc[s] = gscale<SF16>(S, (size_t)wrow[s] * G + kc / a.gs);
-      }
-      half8 av[NB][2][4];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          if constexpr (ROWS32) {
-            const float4* src = reinterpret_cast<const float4*>(a.X + (size_t)arow[b][h] * a.ldx + kc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float4 lo = src[2 * i], hi = src[2 * i + 1];
-              const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-              for (int p = 0; p < 8; ++p) av[b][h][i][p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
-              if (!aok[b][h]) av[b][h][i] = half8{};
-            }
-          } else {
-            const half8* src = reinterpret_cast<const half8*>(a.A + (size_t)arow[b][h] * a.lda + kc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) av[b][h][i] = aok[b][h] ? src[i] : half8{};
-          }
-        }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const __half2 s2 = __float2half2_rn(bsc[s]);
-        const uint32_t wd[4] = {braw[s].x ^ xor4, braw[s].y ^ xor4, braw[s].z ^ xor4, braw[s].w ^ xor4};
+      for (int i = 0; i < kAV; ++i) areg[R][i] = src[i];
+    };
+    auto stage_a = [&](auto set, int buf) {
+      constexpr int R = decltype(set)::value;
+      uint4* dst = reinterpret_cast<uint4*>(lds_dst + buf * kABuf);
+      if constexpr (ROWS32) {
+        // 8 floats -> 8 f16 in MFMA order: position p holds column (p % 2) * 4 + p / 2
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const half8 bv = widen8(wd[i], s2);
+          const float4 lo = areg[R][2 * i], hi = areg[R][2 * i + 1];
+          const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          half8 h;
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              acc[b][h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[b][h][i], bv, acc[b][h][s], 0, 0, 0);
-        }
-      }
-    }
-    // per row block: the waves' partial tiles added in wave order, then stored
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) red[((wave * 2 + h) * 2 + s) * 64 + lane] = acc[b][h][s];
-      __syncthreads();
-      // wave w finishes row half h = w & 1 of sub-tile pair / sub-tile (w >> 1)
-      const int h = wave & 1, s = wave >> 1;
-      auto sum_red = [&](int ss) {
-        f32x4 v = red[((0 * 2 + h) * 2 + ss) * 64 + lane];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) v += red[((w * 2 + h) * 2 + ss) * 64 + lane];
-        return v;
-      };
-      // D layout: lane holds rows 4q .. 4q+3 of column ln of each 16x16 tile
-      if (MODE == MODE_GATE_UP) {
-        if (s == 0) {
-          const f32x4 g = sum_red(0), u = sum_red(1);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int m = mb + 32 * b + 16 * h + 4 * q + j;
-            if (m < m1 && wok[0]) a.act[(size_t)m * a.ldact + perm_pos(nbase + ln)] = (_Float16)(silu(g[j]) * u[j]);
-          }
+          for (int p = 0; p < 8; ++p) h[p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
+          dst[i] = __builtin_bit_cast(uint4, h);
         }
       } else {
-        const f32x4 v = sum_red(s);
+        u32x4* d = reinterpret_cast<u32x4*>(dst);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = mb + 32 * b + 16 * h + 4 * q + j;
-          if (m < m1 && wok[s]) a.Y[(size_t)m * a.ldy + nbase + 16 * s + ln] = v[j];
+        for (int i = 0; i < 4; ++i) d[i] = areg[R][i];
+      }
+    };
+
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) acc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const WeightStep& b, int buf) {
+      const uint8_t* A = lds + buf * kABuf + ln * kARow + 64 * q;
+      __half2 s2[2];
+      uint32_t wd[2][4];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        s2[s] = __float2half2_rn(gscale_value<SF16>(b.s[s]));
+        wd[s][0] = b.w[s].x ^ xor4;
+        wd[s][1] = b.w[s].y ^ xor4;
+        wd[s][2] = b.w[s].z ^ xor4;
+        wd[s][3] = b.w[s].w ^ xor4;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half8 b0 = widen8(wd[0][i], s2[0]), b1 = widen8(wd[1][i], s2[1]);
+        // all four row tiles every step, also past the pass's rows (those
+        // repeat its last row and are not stored): no branch between the
+        // accumulators' updates
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+          const half8 av = *reinterpret_cast<const half8*>(A + rt * 16 * kARow + 16 * i);
+          acc[rt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[rt][0], 0, 0, 0);
+          acc[rt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[rt][1], 0, 0, 0);
         }
       }
-      __syncthreads();  // red is reused by the next block / pass
+    };
+
+    // Activations are loaded two steps ahead (register sets a0 / a1) and
+    // staged at the end of the step before their use; weights one step ahead.
+    // The steady state has unconditional loads (the compiler's wait counts
+    // then keep them in flight), the last one to three steps follow.
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    WeightStep b0, b1;
+    load_a(0, S0{});
+    load_a(nsteps > 1 ? 1 : 0, S1{});
+    load_w(0, b0);
+    stage_a(S0{}, 0);
+    __syncthreads();
+    int st = 0;
+    for (; st + 3 < nsteps; st += 2) {
+      load_a(st + 2, S0{});
+      load_w(st + 1, b1);
+      compute(b0, 0);
+      stage_a(S1{}, 1);
+      __syncthreads();
+      load_a(st + 3, S1{});
+      load_w(st + 2, b0);
+      compute(b1, 1);
+      stage_a(S0{}, 0);
+      __syncthreads();
     }
+    const int left = nsteps - st;  // 1, 2 or 3
+    if (left == 3) {
+      load_a(st + 2, S0{});
+      load_w(st + 1, b1);
+      compute(b0, 0);
+      stage_a(S1{}, 1);
+      __syncthreads();
+      load_w(st + 2, b0);
+      compute(b1, 1);
+      stage_a(S0{}, 0);
+      __syncthreads();
+      compute(b0, 0);
+    } else if (left == 2) {
+      load_w(st + 1, b1);
+      compute(b0, 0);
+      stage_a(S1{}, 1);
+      __syncthreads();
+      compute(b1, 1);
+    } else {
+      compute(b0, 0);
+    }
+
+    // D layout: lane (ln, q) holds rows 4q .. 4q+3 of column ln of each 16x16 tile
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      if (rt >= RT) break;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = mb + 16 * rt + 4 * q + j;
+        if (m >= m1) continue;
+        if (MODE == MODE_GATE_UP) {
+          if (wok[0])
+            a.act[(size_t)m * a.ldact + perm_pos(nbase + 16 * wave + ln)] =
+                (_Float16)(silu(acc[rt][0][j]) * acc[rt][1][j]);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 2; ++s)
+            if (wok[s]) a.Y[(size_t)m * a.ldy + nbase + 32 * wave + 16 * s + ln] = acc[rt][s][j];
+        }
+      }
+    }
+    __syncthreads();  // the LDS tiles are refilled by the next pass
   }
 }
 
-// NBMAX 2: an expert with more than 32 rows is done 64 rows per pass (its
-// weight tile read once for up to 64 rows); the others 32 rows per pass.
-template <int MODE, bool ROWS32, int NBMAX>
+template <int MODE, bool ROWS32>
 __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
-  __shared__ f32x4 red[4 * 2 * 2 * 64];  // 16 KB: per wave, row half, sub-tile, lane
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kABuf];
   // all column tiles of one expert on one XCD: its activation rows stay in that L2
   const int L = xcd_contiguous(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
   const int e = L / gridDim.x, tile = L % gridDim.x;
   const int m0 = a.table ? a.eoff[e] : 0, m1 = a.table ? a.eoff[e + 1] : a.single_rows;
-  if (m0 >= m1) return;
-  const int per_tile = MODE == MODE_GATE_UP ? 16 : 32;
-  const int nbase = tile * per_tile;
+  if (m0 >= m1) return;  // the whole workgroup: before any barrier
+  const int nbase = tile * (MODE == MODE_GATE_UP ? 64 : 128);
   const ExpertDesc d = a.table ? a.table[e] : a.single;
   const uint8_t* Wt = a.which ? d.dn_w : d.gu_w;
   const void* S = a.which ? d.dn_s : d.gu_s;
   const uint32_t xor4 = d.xor8 * 0x01010101u;
-  if (NBMAX == 2 && m1 - m0 > 32) {
-    if (d.s_f16) gemm_body<MODE, true, ROWS32, 2>(a, Wt, S, xor4, m0, m1, nbase, red);
-    else gemm_body<MODE, false, ROWS32, 2>(a, Wt, S, xor4, m0, m1, nbase, red);
-  } else {
-    if (d.s_f16) gemm_body<MODE, true, ROWS32, 1>(a, Wt, S, xor4, m0, m1, nbase, red);
-    else gemm_body<MODE, false, ROWS32, 1>(a, Wt, S, xor4, m0, m1, nbase, red);
-  }
+  if (d.s_f16) gemm_tile<MODE, true, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, lds);
+  else gemm_tile<MODE, false, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, lds);
 }
 
 // ------------------------------------------------------------------ combine
@@ -522,24 +591,20 @@ int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Floa
   return check_launch("gather rows (f16)");
 }
 
-int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st, int rows_hint) {
+int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
   if (nexp <= 0) return MOE_OK;
-  const int per_tile = mode == MODE_GATE_UP ? 16 : 32;
+  const int per_tile = mode == MODE_GATE_UP ? 64 : 128;
   const int n = mode == MODE_GATE_UP ? a.I : a.N;
   dim3 grid((n + per_tile - 1) / per_tile, nexp);
-  // 64-row passes cost occupancy: only when some experts may hold > 32 rows
-  const bool two = rows_hint > 16;
   auto go = [&](auto k) { hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a); };
   if (a.rows32) {
-    if (mode == MODE_PLAIN) two ? go(gemm_q4_kernel<MODE_PLAIN, true, 2>) : go(gemm_q4_kernel<MODE_PLAIN, true, 1>);
-    else if (mode == MODE_GATE_UP)
-      two ? go(gemm_q4_kernel<MODE_GATE_UP, true, 2>) : go(gemm_q4_kernel<MODE_GATE_UP, true, 1>);
+    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, true>);
+    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, true>);
     else return set_error(MOE_EINVAL, "int4 grouped GEMM: the down product takes f16 activations");
   } else {
-    if (mode == MODE_PLAIN) two ? go(gemm_q4_kernel<MODE_PLAIN, false, 2>) : go(gemm_q4_kernel<MODE_PLAIN, false, 1>);
-    else if (mode == MODE_GATE_UP)
-      two ? go(gemm_q4_kernel<MODE_GATE_UP, false, 2>) : go(gemm_q4_kernel<MODE_GATE_UP, false, 1>);
-    else two ? go(gemm_q4_kernel<MODE_DOWN, false, 2>) : go(gemm_q4_kernel<MODE_DOWN, false, 1>);
+    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, false>);
+    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, false>);
+    else go(gemm_q4_kernel<MODE_DOWN, false>);
   }
   return check_launch("int4 grouped GEMM");
 }
