@@ -271,11 +271,9 @@ namespace moe {
 static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // largest token count one grouping workgroup takes (its bitsets live in LDS)
-static int max_group_tokens(int E) {
-  const size_t lds = 56 * 1024;  // of 64 KB: the kernel's own counters take the rest
-  const size_t words = lds / (2 * sizeof(uint32_t) * (size_t)E);
-  return (int)(words * 32);
-}
+// moe_prefill_layer reads a prompt in passes of at most this many tokens (the
+// workspace holds one pass)
+static constexpr int kPrefillPass = 2048;
 
 struct PrefillWs {
   float* logits;
@@ -399,8 +397,7 @@ MOE_API int moe_route(const float* logits, int T, int E, int k, int normalize, i
 MOE_API int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts,
                                 int* pos, int* experts, int* offsets, int* n_used, void* stream) {
   REQUIRE(E > 0 && E <= 1024 && k > 0 && T >= 0, "moe_group_by_expert: T=%d k=%d E=%d", T, k, E);
-  REQUIRE(T <= max_group_tokens(E), "moe_group_by_expert: %d tokens exceed one pass (%d for %d experts)", T,
-          max_group_tokens(E), E);
+  REQUIRE((long)T * k <= (1L << 30), "moe_group_by_expert: %d x %d picks", T, k);
   REQUIRE(idx && w && eoff && rows && wts && pos && experts && offsets && n_used, "moe_group_by_expert: null pointer");
   return run_group(idx, w, T, k, E, eoff, rows, wts, pos, experts, offsets, n_used, as_stream(stream));
 }
@@ -431,7 +428,7 @@ MOE_API int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* tab
 
 MOE_API size_t moe_prefill_workspace(int T, int E, int k, int H, int I) {
   if (T <= 0 || E <= 0 || k <= 0 || H <= 0 || I <= 0) return 0;
-  const int pass = T < max_group_tokens(E) ? T : max_group_tokens(E);
+  const int pass = T < kPrefillPass ? T : kPrefillPass;
   return prefill_layout(nullptr, pass, E, k, H, I).bytes;
 }
 
@@ -450,15 +447,21 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
   REQUIRE(aligned(workspace, 256), "moe_prefill_layer: workspace must be 256-byte aligned");
   hipStream_t st = as_stream(stream);
   const ExpertDesc* tab = reinterpret_cast<const ExpertDesc*>(table);
-  const int pass = max_group_tokens(E);
+  const int pass = kPrefillPass;
   for (int t0 = 0; t0 < T; t0 += pass) {  // passes of at most `pass` tokens, as moelan/model.py:640-666
     const int n = T - t0 < pass ? T - t0 : pass;
     PrefillWs w = prefill_layout(workspace, n, E, k, H, I);
     const float* xp = x + (size_t)t0 * ldx;
-    const int nz = router_slices(n, E, H);
-    int rc = run_router_partials(xp, ldx, router, n, E, H, nz, w.logits, st);
+    int rc, nz = 1;
+    if (router_mfma_ok(xp, ldx, router, H)) {
+      nz = router_mfma_slices(n, E, H, router_slices(n, E, H));
+      rc = run_router_mfma(xp, ldx, router, n, E, H, nz, w.logits, st);
+    } else {
+      nz = router_slices(n, E, H);
+      rc = run_router_partials(xp, ldx, router, n, E, H, nz, w.logits, st);
+    }
     if (!rc) rc = run_route(w.logits, nz, n, E, k, normalize, w.idx, w.w, st);
-    if (!rc) rc = run_group(w.idx, w.w, n, k, E, w.eoff, w.rows, w.wts, w.pos, w.experts, w.offsets, w.n_used, st);
+    if (!rc) rc = run_group(w.idx, w.w, n, k, E, w.eoff, w.rows, w.wts, w.pos, nullptr, nullptr, nullptr, st);
     if (!rc) rc = grouped_ffn(xp, ldx, tab, E, w.eoff, w.rows, n * k, H, I, gs, w.xs, w.act, w.y, H, st);
     if (!rc) rc = run_token_combine(w.y, H, w.pos, w.wts, n, k, H, out + (size_t)t0 * ldo, ldo, st);
     if (rc) return rc;

@@ -31,11 +31,17 @@ struct GemmArgs {
 int router_slices(int T, int E, int H);
 int run_router_partials(const float* x, int ldx, const float* R, int T, int E, int H, int nz, float* part,
                         hipStream_t st);
-// scratch: router_slices(T, E, H) * T * E floats, or null for one slice
+// the f32 MFMA router applies: H a multiple of 64, rows 16-byte aligned
+bool router_mfma_ok(const float* x, int ldx, const float* R, int H);
+// K slices for the MFMA router (1 unless the tiles are few; at most max_slices)
+int router_mfma_slices(int T, int E, int H, int max_slices);
+// part: nz slices of T x E partial logits (nz = 1: the logits)
+int run_router_mfma(const float* x, int ldx, const float* R, int T, int E, int H, int nz, float* part, hipStream_t st);
+// MFMA when it applies, else split K: scratch router_slices(T, E, H) * T * E floats (null: one slice)
 int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, float* scratch,
                       hipStream_t st);
 int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st);
-size_t group_lds_bytes(int T, int E);
+// experts / offsets / n_used may be null (not produced)
 int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
               int* experts, int* offsets, int* n_used, hipStream_t st);
 int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, hipStream_t st);

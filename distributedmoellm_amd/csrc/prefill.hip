@@ -73,6 +73,62 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* x, int 
     }
 }
 
+// Router logits on the f32 matrix cores: block (t0, e0, z) computes the
+// 16 x 16 tile (tokens x experts) of x . R^T over K slice z (kslice columns);
+// its W waves take equal parts of the slice and their partial tiles are added
+// through LDS in wave order; several slices are summed in slice order by the
+// consumer (deterministic). Per 16 columns a lane loads a float4 of its token
+// row and of its expert row and feeds them to 4 MFMAs (v_mfma_f32_16x16x4_f32;
+// MFMA j takes column 4q + j of each 16, for A and B alike). kslice a multiple
+// of 16 W, rows 16-byte aligned. Rows / experts past T / E repeat the last
+// one and are not stored.
+template <int W, int CH>
+__global__ __launch_bounds__(64 * W) void router_mfma_kernel(const float* x, int ldx, const float* R, int T, int E,
+                                                             int H, int kslice, float* part) {
+  __shared__ f32x4 red[W][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 15, q = lane >> 4;
+  // the expert tiles (and slices) of one token tile on one XCD: its rows of x
+  // come from HBM once and then from that XCD's L2
+  const int L = xcd_contiguous(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                               gridDim.x * gridDim.y * gridDim.z);
+  const int z = L % gridDim.z, e0 = (L / gridDim.z) % gridDim.y * 16, t0 = L / (gridDim.z * gridDim.y) * 16;
+  const int t = min(t0 + ln, T - 1), e = min(e0 + ln, E - 1);
+  const int kw = kslice / W, kb = z * kslice + wave * kw;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * ldx + kb) + q;
+  const float4* rr = reinterpret_cast<const float4*>(R + (size_t)e * H + kb) + q;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // chunks of CH x 16 columns (kw is a multiple): all of a chunk's loads first
+  for (int k0 = 0; k0 < kw; k0 += 16 * CH) {
+    float4 a[CH], b[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      a[j] = xr[(k0 + 16 * j) / 4];
+      b[j] = rr[(k0 + 16 * j) / 4];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the chunk ahead of its MFMAs
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].x, b[j].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].y, b[j].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].z, b[j].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].w, b[j].w, acc, 0, 0, 0);
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 v = red[0][lane];
+#pragma unroll
+  for (int w = 1; w < W; ++w) v += red[w][lane];
+  float* dst = part + (size_t)z * T * E;
+  // D layout: lane (ln, q) holds tokens 4q .. 4q+3 of expert column ln
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tt = t0 + 4 * q + j, ee = e0 + ln;
+    if (tt < T && ee < E) dst[(size_t)tt * E + ee] = v[j];
+  }
+}
+
 __global__ void sum_slices_kernel(const float* part, int nz, long n, float* out) {
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
     float v = part[i];
@@ -156,64 +212,124 @@ __global__ __launch_bounds__(256) void route_kernel(const float* logits, int nz,
 
 // ------------------------------------------------------------------ grouping
 
-// Stable grouping of the (token, pick) pairs by expert in one workgroup:
-// per-expert token bitsets (atomicOr: order-free), per-word prefix counts, a
-// scan over experts; a pair's place is its expert's offset plus the number of
-// earlier tokens in the bitset. Invalid expert ids are dropped (pos = -1).
-__global__ __launch_bounds__(1024) void group_kernel(const int* idx, const float* w, int T, int k, int E, int W,
-                                                     int* eoff, int* rows, float* wts, int* pos, int* experts,
-                                                     int* offsets, int* n_used) {
-  extern __shared__ uint32_t sh[];
-  uint32_t* bits = sh;          // [E][W]
-  uint32_t* pre = sh + E * W;   // [E][W]
-  __shared__ int tot[1025];
-  const int tid = threadIdx.x, nt = blockDim.x;
-  for (int i = tid; i < E * W; i += nt) bits[i] = 0u;
-  __syncthreads();
-  const int P = T * k;
-  for (int p = tid; p < P; p += nt) {
-    const int e = idx[p], t = p / k;
-    if (e >= 0 && e < E) atomicOr(&bits[e * W + (t >> 5)], 1u << (t & 31));
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += nt) {
-    int run = 0;
-    for (int wd = 0; wd < W; ++wd) {
-      pre[e * W + wd] = run;
-      run += __popc(bits[e * W + wd]);
+// Stable grouping of the P = T*k picks by expert, one block per expert: a
+// pick's place is its expert's offset (the number of picks of lower expert
+// ids) plus the number of earlier picks of the same expert -- exactly
+// argsort(idx.ravel(), kind="stable"). The block stages the pick ids and
+// weights in LDS in chunks; its 4 waves take quarters of each chunk, count
+// (per lane, then summed), add the earlier quarters' counts (LDS, in order)
+// and write the places in pick order with ballots. Invalid expert ids are
+// dropped (pos = -1, written by the block of expert 0).
+constexpr int kGroupChunk = 4096;  // picks staged at once (ids and weights: 32 KB)
+
+__global__ __launch_bounds__(256) void group_kernel(const int* idx, const float* w, int P, int k, int E, int* eoff,
+                                                    int* rows, float* wts, int* pos) {
+  __shared__ int ids[kGroupChunk];
+  __shared__ float wv[kGroupChunk];
+  __shared__ int cnt[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x;
+  const uint64_t below = (1ull << lane) - 1ull;
+  // chunk c0 .. c0+n into LDS, padded with id -1 up to a multiple of 1024; each
+  // thread's loads are issued together (16 picks per thread)
+  auto stage = [&](int c0, int n) {
+    __syncthreads();
+    int iv[16];
+    float fv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = threadIdx.x + 256 * j, p = c0 + i;
+      const bool in = i < n;
+      iv[j] = in ? idx[p] : -1;
+      fv[j] = in ? w[p] : 0.f;
     }
-    tot[e] = run;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      ids[threadIdx.x + 256 * j] = iv[j];
+      wv[threadIdx.x + 256 * j] = fv[j];
+    }
+    __syncthreads();
+  };
+  // wave quarters of a chunk of n picks: [wave * q, (wave + 1) * q), q a multiple of 64
+  auto quarter = [&](int n) { return ((n + 255) / 256) * 64; };
+  // pass 1: per-wave counts of lower ids and of e over all chunks
+  int lt = 0, eq = 0;
+  for (int c0 = 0; c0 < P; c0 += kGroupChunk) {
+    const int n = min(kGroupChunk, P - c0), qn = quarter(n);
+    stage(c0, n);
+    for (int i0 = wave * qn; i0 < (wave + 1) * qn; i0 += 64) {
+      const int id = ids[i0 + lane];
+      lt += (id >= 0 && id < e) ? 1 : 0;
+      eq += id == e ? 1 : 0;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    lt += __shfl_xor(lt, off, 64);
+    eq += __shfl_xor(eq, off, 64);
+  }
+  if (lane == 0) {
+    cnt[0][wave] = lt;
+    cnt[1][wave] = eq;
   }
   __syncthreads();
-  if (tid == 0) {  // E <= 1024 counts: a serial scan, plus the compact list
-    int run = 0, nu = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = tot[e];
-      eoff[e] = run;
-      if (c > 0) {
-        experts[nu] = e;
-        offsets[nu] = run;
-        ++nu;
+  const int below_e = cnt[0][0] + cnt[0][1] + cnt[0][2] + cnt[0][3];
+  if (threadIdx.x == 0) {
+    eoff[e] = below_e;
+    if (e == E - 1) eoff[E] = below_e + cnt[1][0] + cnt[1][1] + cnt[1][2] + cnt[1][3];
+  }
+  // pass 2: places in pick order. Within a chunk, wave w starts after the
+  // earlier waves' picks of e in that chunk: counted again per chunk
+  int run = below_e;
+  for (int c0 = 0; c0 < P; c0 += kGroupChunk) {
+    const int n = min(kGroupChunk, P - c0), qn = quarter(n);
+    if (P > kGroupChunk) stage(c0, n);  // one chunk: still in LDS
+    int mine_n = 0;
+    for (int i0 = wave * qn; i0 < (wave + 1) * qn; i0 += 64) mine_n += ids[i0 + lane] == e ? 1 : 0;
+    for (int off = 32; off > 0; off >>= 1) mine_n += __shfl_xor(mine_n, off, 64);
+    __syncthreads();
+    if (lane == 0) cnt[1][wave] = mine_n;
+    __syncthreads();
+    int r = run;
+    for (int v = 0; v < wave; ++v) r += cnt[1][v];
+    for (int i0 = wave * qn; i0 < (wave + 1) * qn; i0 += 64) {
+      const int i = i0 + lane, p = c0 + i;
+      const int id = ids[i];
+      const bool mine = id == e;
+      const uint64_t m = __ballot(mine);
+      if (mine) {
+        const int q = r + __popcll(m & below);
+        rows[q] = p / k;
+        wts[q] = wv[i];
+        pos[p] = q;
       }
-      run += c;
+      if (e == 0 && i < n && (id < 0 || id >= E)) pos[p] = -1;
+      r += __popcll(m);
     }
-    eoff[E] = run;
-    offsets[nu] = run;
-    *n_used = nu;
+    run += cnt[1][0] + cnt[1][1] + cnt[1][2] + cnt[1][3];
   }
+}
+
+// The experts that received picks, ascending, with their ranges (E <= 1024).
+__global__ __launch_bounds__(1024) void used_experts_kernel(const int* eoff, int E, int* experts, int* offsets,
+                                                            int* n_used) {
+  __shared__ int wave_used[16];
+  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
+  const bool used = e < E && eoff[e + 1] > eoff[e];
+  const uint64_t m = __ballot(used);
+  if (lane == 0) wave_used[wave] = __popcll(m);
   __syncthreads();
-  for (int p = tid; p < P; p += nt) {
-    const int e = idx[p], t = p / k;
-    if (e < 0 || e >= E) {
-      pos[p] = -1;
-      continue;
-    }
-    const int wd = t >> 5, b = t & 31;
-    const int r = pre[e * W + wd] + __popc(bits[e * W + wd] & ((1u << b) - 1u));
-    const int q = eoff[e] + r;
-    rows[q] = t;
-    wts[q] = w[p];
-    pos[p] = q;
+  int base = 0;
+  for (int i = 0; i < wave; ++i) base += wave_used[i];
+  if (used) {
+    const int slot = base + __popcll(m & ((1ull << lane) - 1ull));
+    experts[slot] = e;
+    offsets[slot] = eoff[e];
+  }
+  if (e == 0) {
+    int total = 0;
+    for (int i = 0; i < 16; ++i) total += wave_used[i];
+    *n_used = total;
+    offsets[total] = eoff[E];
   }
 }
 
@@ -503,36 +619,55 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
 
 // out[t] = sum over t's picks in ascending expert order (= ascending pair
 // position) of w * y[pos]; overwrites out (the layer output starts at zero).
+// One block per token: the first wave ranks the token's (at most 16) picks by
+// position -- rank = number of smaller positions, positions being distinct --
+// and puts them in LDS in that order; then each thread sums float4 columns
+// over the picks in order.
 __global__ __launch_bounds__(256) void token_combine_kernel(const float* y, int ldy, const int* pos, const float* wts,
-                                                            int k, int H, float* out, int ldo) {
-  const int t = blockIdx.y;
-  int pp[16];
-  int n = 0;
-  for (int j = 0; j < k && j < 16; ++j) {
-    const int p = pos[(size_t)t * k + j];
-    if (p < 0) continue;
-    int i = n++;
-    while (i > 0 && pp[i - 1] > p) {
-      pp[i] = pp[i - 1];
-      --i;
+                                                            int k, int H, float* out, int ldo, int vec4) {
+  __shared__ int sp[16];
+  __shared__ float sw[16];
+  __shared__ int sn;
+  const int t = blockIdx.x;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const bool mine = lane < k && lane < 16;
+    const int p = mine ? pos[(size_t)t * k + lane] : -1;
+    int rank = 0;
+    for (int i = 0; i < k && i < 16; ++i) {
+      const int pi = __shfl(p, i, 64);
+      rank += (pi >= 0 && pi < p) ? 1 : 0;
     }
-    pp[i] = p;
+    const uint64_t valid = __ballot(mine && p >= 0);
+    if (mine && p >= 0) {
+      sp[rank] = p;
+      sw[rank] = wts[p];
+    }
+    if (lane == 0) sn = __popcll(valid);
   }
-  for (int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4; c < H; c += gridDim.x * blockDim.x * 4) {
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int i = 0; i < n; ++i) {
-      const float w = wts[pp[i]];
-      const float* yp = y + (size_t)pp[i] * ldy + c;
-      a.x += w * yp[0];
-      if (c + 1 < H) a.y += w * yp[1];
-      if (c + 2 < H) a.z += w * yp[2];
-      if (c + 3 < H) a.w += w * yp[3];
+  __syncthreads();
+  const int n = sn;
+  float* dst = out + (size_t)t * ldo;
+  if (vec4) {
+    for (int c = threadIdx.x * 4; c < H; c += 1024) {
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+      for (int i = 0; i < n; ++i) {
+        const float w = sw[i];
+        const float4 v = *reinterpret_cast<const float4*>(y + (size_t)sp[i] * ldy + c);
+        a.x += w * v.x;
+        a.y += w * v.y;
+        a.z += w * v.z;
+        a.w += w * v.w;
+      }
+      *reinterpret_cast<float4*>(dst + c) = a;
     }
-    float* dst = out + (size_t)t * ldo + c;
-    dst[0] = a.x;
-    if (c + 1 < H) dst[1] = a.y;
-    if (c + 2 < H) dst[2] = a.z;
-    if (c + 3 < H) dst[3] = a.w;
+  } else {
+    for (int c = threadIdx.x; c < H; c += 256) {
+      float a = 0.f;
+      for (int i = 0; i < n; ++i) a += sw[i] * y[(size_t)sp[i] * ldy + c];
+      dst[c] = a;
+    }
   }
 }
 
@@ -559,8 +694,43 @@ int run_router_partials(const float* x, int ldx, const float* R, int T, int E, i
   return check_launch("router logits");
 }
 
+bool router_mfma_ok(const float* x, int ldx, const float* R, int H) {
+  return H % 64 == 0 && ldx % 4 == 0 && aligned(x, 16) && aligned(R, 16);
+}
+
+// K slices of the MFMA router: one, unless the token x expert tiles are too
+// few to fill the chip (then up to max_slices, each of at least 1024 columns)
+int router_mfma_slices(int T, int E, int H, int max_slices) {
+  const long tiles = (long)((T + 15) / 16) * ((E + 15) / 16);
+  int z = 1;
+  while (2 * z <= max_slices && tiles * z < 256 && H % (512 * z) == 0 && H / (2 * z) >= 1024) z *= 2;
+  return z;
+}
+
+int run_router_mfma(const float* x, int ldx, const float* R, int T, int E, int H, int nz, float* part, hipStream_t st) {
+  if (T <= 0) return MOE_OK;
+  const dim3 grid((T + 15) / 16, (E + 15) / 16, nz);
+  const int kslice = H / nz;
+  // W waves per block, each kslice / W columns in chunks of CH x 16
+  if (kslice % (16 * 128) == 0)
+    hipLaunchKernelGGL((router_mfma_kernel<16, 8>), grid, dim3(1024), 0, st, x, ldx, R, T, E, H, kslice, part);
+  else if (kslice % (4 * 128) == 0)
+    hipLaunchKernelGGL((router_mfma_kernel<4, 8>), grid, dim3(256), 0, st, x, ldx, R, T, E, H, kslice, part);
+  else
+    hipLaunchKernelGGL((router_mfma_kernel<4, 1>), grid, dim3(256), 0, st, x, ldx, R, T, E, H, kslice, part);
+  return check_launch("router logits (MFMA)");
+}
+
 int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, float* scratch,
                       hipStream_t st) {
+  if (router_mfma_ok(x, ldx, R, H)) {
+    const int nz = scratch ? router_mfma_slices(T, E, H, router_slices(T, E, H)) : 1;
+    int rc = run_router_mfma(x, ldx, R, T, E, H, nz, nz > 1 ? scratch : logits, st);
+    if (rc || nz == 1) return rc;
+    const long n = (long)T * E;
+    hipLaunchKernelGGL(sum_slices_kernel, dim3(blocks_for(n)), dim3(256), 0, st, scratch, nz, n, logits);
+    return check_launch("router logits (slice sum)");
+  }
   const int nz = scratch ? router_slices(T, E, H) : 1;
   int rc = run_router_partials(x, ldx, R, T, E, H, nz, nz > 1 ? scratch : logits, st);
   if (rc || nz == 1) return rc;
@@ -574,14 +744,13 @@ int run_route(const float* logits, int nz, int T, int E, int k, int normalize, i
   return check_launch("softmax top-k");
 }
 
-size_t group_lds_bytes(int T, int E) { return (size_t)2 * E * ((T + 31) / 32) * sizeof(uint32_t); }
-
 int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
               int* experts, int* offsets, int* n_used, hipStream_t st) {
-  const int W = (T + 31) / 32;
-  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), group_lds_bytes(T, E), st, idx, w, T, k, E, W, eoff, rows, wts,
-                     pos, experts, offsets, n_used);
-  return check_launch("group by expert");
+  hipLaunchKernelGGL(group_kernel, dim3(E), dim3(256), 0, st, idx, w, T * k, k, E, eoff, rows, wts, pos);
+  if (int rc = check_launch("group by expert")) return rc;
+  if (!experts) return MOE_OK;
+  hipLaunchKernelGGL(used_experts_kernel, dim3(1), dim3(1024), 0, st, eoff, E, experts, offsets, n_used);
+  return check_launch("group by expert (used experts)");
 }
 
 int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, hipStream_t st) {
@@ -612,8 +781,9 @@ int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
 int run_token_combine(const float* y, int ldy, const int* pos, const float* wts, int T, int k, int H, float* out,
                       int ldo, hipStream_t st) {
   if (T <= 0) return MOE_OK;
-  const int gx = (H + 1023) / 1024;
-  hipLaunchKernelGGL(token_combine_kernel, dim3(gx, T), dim3(256), 0, st, y, ldy, pos, wts, k, H, out, ldo);
+  if (k > 16) return set_error(MOE_EINVAL, "token combine: k=%d (at most 16 picks per token)", k);
+  const int vec4 = H % 4 == 0 && ldy % 4 == 0 && ldo % 4 == 0 && aligned(y, 16) && aligned(out, 16);
+  hipLaunchKernelGGL(token_combine_kernel, dim3(T), dim3(256), 0, st, y, ldy, pos, wts, k, H, out, ldo, vec4);
   return check_launch("token combine");
 }
 

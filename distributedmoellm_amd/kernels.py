@@ -414,7 +414,8 @@ def group_by_expert(idx, w, num_experts: int | None = None, with_pos: bool = Fal
     _lib.call("moe_group_by_expert", _ptr(idd), _ptr(wd), T, k, E, _ptr(eoff), _ptr(rows), _ptr(wts), _ptr(pos),
               _ptr(experts), _ptr(offsets), _ptr(n_used), stream_handle())
     nu = int(n_used.item())
-    res = (experts[:nu], offsets[:nu + 1], rows, wts)
+    total = int(offsets[nu].item())  # picks with a valid expert id (all of them for router output)
+    res = (experts[:nu], offsets[:nu + 1], rows[:total], wts[:total])
     if not is_device(idx):
         res = tuple(t.cpu().numpy() for t in res)
     if with_pos:

@@ -161,8 +161,8 @@ int moe_route(const float* logits, int T, int E, int k, int normalize, int* idx,
  * moelan/model.py:226-236: experts[0..*n_used) ascending with their pick
  * ranges offsets[0..*n_used]; eoff[E+1] the same ranges for every expert id;
  * rows[q] / wts[q] the token and weight of grouped pick q; pos[t*k+j] where
- * pick j of token t went (-1 for an expert id outside 0..E-1). One pass holds
- * T <= 65536*8/E tokens. All device arrays. */
+ * pick j of token t went (-1 for an expert id outside 0..E-1). E <= 1024.
+ * All device arrays. */
 int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
                         int* experts, int* offsets, int* n_used, void* stream);
 
@@ -178,7 +178,7 @@ size_t moe_q4_grouped_ffn_workspace(int P, int H, int I);
 int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* table, int nexp, const int* eoff, const int* rows,
                        int P, int H, int I, int gs, float* y, int ldy, void* workspace, size_t ws_bytes, void* stream);
 
-/* Bytes of workspace moe_prefill_layer needs (one pass of tokens). */
+/* Bytes of workspace moe_prefill_layer needs (one pass of at most 2048 tokens). */
 size_t moe_prefill_workspace(int T, int E, int k, int H, int I);
 
 /* One MoE layer over T tokens: router logits, route, group, grouped expert

@@ -81,7 +81,8 @@ def test_route_matches_oracle_on_identical_logits(kernels, E, k):
         assert len(ties) <= 2
 
 
-@pytest.mark.parametrize("T,k,E", [(512, 8, 128), (1792, 8, 128), (37, 4, 16), (1, 2, 8)])
+@pytest.mark.parametrize("T,k,E", [(512, 8, 128), (1792, 8, 128), (4000, 8, 128), (37, 4, 16), (1, 2, 8),
+                                   (300, 6, 61), (64, 8, 1024)])
 def test_group_by_expert_bit_exact(kernels, T, k, E):
     rng = np.random.default_rng(T)
     idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
@@ -100,10 +101,28 @@ def test_group_by_expert_bit_exact(kernels, T, k, E):
     assert np.array_equal(np.bincount(flat, minlength=E), np.diff(eoff))
 
 
-def test_group_pass_limit_is_an_error(kernels):
-    idx = np.zeros((4000, 8), np.int32) + np.arange(8, dtype=np.int32)
-    with pytest.raises(RuntimeError, match="exceed one pass"):
-        kernels.group_by_expert(idx, np.ones((4000, 8), np.float32), 128)
+def test_group_drops_invalid_ids_and_keeps_pick_order(kernels):
+    """Ids outside 0..E-1 are dropped (pos -1); a token naming one expert twice
+    keeps both picks in pick order (stable argsort of the flat ids)."""
+    rng = np.random.default_rng(5)
+    T, k, E = 200, 4, 32
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    idx[3, 1] = -1
+    idx[10, 0] = E
+    idx[11, 2] = 1000
+    idx[20] = [7, 7, 2, 7]
+    w = rng.random((T, k)).astype(np.float32)
+    got = kernels.group_by_expert(torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), E, with_pos=True)
+    experts, offsets, rows, weights = (t.cpu().numpy() for t in got[:4])
+    eoff, pos = (t.cpu().numpy() for t in got[4])
+    flat = idx.reshape(-1)
+    ok = (flat >= 0) & (flat < E)
+    assert np.array_equal(pos[~ok], np.full((~ok).sum(), -1))
+    order = np.argsort(np.where(ok, flat, E + 1), kind="stable")[: ok.sum()]
+    assert np.array_equal(rows, order // k) and np.array_equal(weights, w.reshape(-1)[order])
+    assert np.array_equal(pos[order], np.arange(ok.sum()))
+    assert np.array_equal(experts, np.unique(flat[ok]))
+    assert eoff[-1] == ok.sum() and offsets[-1] == ok.sum()
 
 
 # ---------------------------------------------------------------- grouped expert FFN
