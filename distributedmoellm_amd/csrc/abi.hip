@@ -363,6 +363,10 @@ static int check_mfma_shape(const char* who, int H, int I, int gs) {
   REQUIRE(H > 0 && I > 0 && gs > 0, "%s: H=%d, I=%d and gs=%d must be positive", who, H, I, gs);
   if (H % 128 != 0 || I % 128 != 0)
     return set_error(MOE_EUNSUPPORTED, "%s: H=%d and I=%d must be multiples of 128", who, H, I);
+  // the kernels' group index arithmetic holds for rows below 2^20 columns,
+  // their byte offsets for matrices below 4 GiB
+  if (H >= (1 << 20) || I >= (1 << 20) || (size_t)H * I >= (1ull << 32))
+    return set_error(MOE_EUNSUPPORTED, "%s: H=%d and I=%d must be below 2^20, their product below 2^32", who, H, I);
   if (gs % 32 != 0 || H % gs != 0 || I % gs != 0)
     return set_error(MOE_EUNSUPPORTED, "%s: group size %d must be a multiple of 32 dividing H=%d and I=%d", who, gs,
                      H, I);
@@ -475,6 +479,8 @@ MOE_API int moe_q4_gemm(const float* x, int n, const uint8_t* raw, const void* s
   REQUIRE(gs > 0 && gs % 32 == 0 && I % gs == 0, "moe_q4_gemm: group size %d must be a multiple of 32 dividing I=%d",
           gs, I);
   REQUIRE(n >= 0, "moe_q4_gemm: n=%d", n);
+  if (I >= (1 << 20) || (size_t)O * I >= (1ull << 33))
+    return set_error(MOE_EUNSUPPORTED, "moe_q4_gemm: I=%d must be below 2^20 and the matrix below 4 GiB (O=%d)", I, O);
   if (n == 0) return MOE_OK;
   REQUIRE(x && raw && s && y, "moe_q4_gemm: null pointer");
   REQUIRE(aligned(x, 16), "moe_q4_gemm: x must be 16-byte aligned");

@@ -355,41 +355,53 @@ __global__ void gather_f16_kernel(const float* x, int ldx, const int* rows, int 
 // ------------------------------------------------------------------ grouped GEMM
 
 // 8 nibbles (one dword, columns 0..7 of a 32-column run) -> four f16 pairs
-// (0,4) (1,5) (2,6) (3,7), each (u - 8) * s rounded once to f16.
-__device__ __forceinline__ half8 widen8(uint32_t w, __half2 s2) {
-  const uint32_t m = 0x000F000Fu, magic = 0x64006400u;  // f16 1024 + u
-  const __half2 off = __halves2half2(__float2half(1032.f), __float2half(1032.f));
-  uint32_t r[4];
-  r[0] = (w & m) | magic;
-  r[1] = ((w >> 4) & m) | magic;
-  r[2] = ((w >> 8) & m) | magic;
-  r[3] = ((w >> 12) & m) | magic;
+// (0,4) (1,5) (2,6) (3,7), each (u - 8) * s rounded once to f16. A nibble in
+// bits 0..3 of a half under exponent 2^10 (0x6400) reads 1024 + u; one in bits
+// 4..7 under exponent 2^6 (0x5400, mantissa unit 1/16) reads 64 + u, so one
+// shift serves all four pairs. c0 / c1 = (xor & mask) | exponent: the XOR that
+// turns stored nibbles v into u = v + 8 rides along with the exponent bits.
+__device__ __forceinline__ uint32_t widen_c0(uint32_t xor4) { return (xor4 & 0x000F000Fu) | 0x64006400u; }
+__device__ __forceinline__ uint32_t widen_c1(uint32_t xor4) { return (xor4 & 0x00F000F0u) | 0x54005400u; }
+
+__device__ __forceinline__ half8 widen8(uint32_t w, __half2 s2, uint32_t c0, uint32_t c1) {
+  const uint32_t w8 = w >> 8;
+  const uint32_t r[4] = {(w & 0x000F000Fu) ^ c0, (w & 0x00F000F0u) ^ c1, (w8 & 0x000F000Fu) ^ c0,
+                         (w8 & 0x00F000F0u) ^ c1};
+  const __half2 off_lo = __halves2half2(__float2half(1032.f), __float2half(1032.f));
+  const __half2 off_hi = __halves2half2(__float2half(72.f), __float2half(72.f));
   half8 out;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     __half2 h = __builtin_bit_cast(__half2, r[i]);
-    h = __hmul2(__hsub2(h, off), s2);  // exact (u - 8), then one rounding
-    const uint32_t b = __builtin_bit_cast(uint32_t, h);
-    out[2 * i] = __builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
-    out[2 * i + 1] = __builtin_bit_cast(_Float16, (uint16_t)(b >> 16));
+    h = __hmul2(__hsub2(h, (i & 1) ? off_hi : off_lo), s2);  // exact (u - 8), then one rounding
+    const uint32_t bits = __builtin_bit_cast(uint32_t, h);
+    out[2 * i] = __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+    out[2 * i + 1] = __builtin_bit_cast(_Float16, (uint16_t)(bits >> 16));
   }
   return out;
 }
 
 // A workgroup computes the output tile of one expert for up to 64 of its rows
-// (4 row tiles of 16) and 128 weight rows: wave w owns weight rows 32w ..
-// 32w+31 of the tile as two 16-row sub-tiles.
+// and 128 weight rows: wave w owns weight rows 32w .. 32w+31 of the tile as
+// two 16-row sub-tiles.
 //   MODE_PLAIN / MODE_DOWN: sub-tile s = weight rows n0 + 32w + 16s ..; y f32
 //   MODE_GATE_UP: sub-tile 0 = gate rows j0 + 16w .., 1 = the up rows I + j0 +
 //                 16w ..; act = silu(gate) * up as f16, columns in MFMA order
-// K advances in steps of 128. The step's activation tile (64 rows x 128
-// f16 = 16 KB) is staged in LDS once and read by all four waves (double
-// buffered, one barrier per step; wave w loads rows 16w .. 16w+15). Each
-// lane streams 16 bytes (32 nibbles) of each of its two weight rows per step,
-// issued one step ahead, widens them to f16 with the group scale once and
-// feeds them to every row tile: 2 x 4 x RT MFMAs per step. Rows of a pass past
-// the expert's last row repeat its last row and are not stored. An expert
-// with more than 64 rows is done in passes (its weight tile read again).
+// K advances in steps of 128 columns.
+//  * Activations: the step's tile (16 RT rows x 128 f16) is staged in LDS once
+//    and read by all four waves (double buffered, one barrier per step, loaded
+//    two steps ahead; 16 threads read one row's 256 contiguous bytes). RT, the
+//    row tiles of the pass, is a compile-time constant of the pass's code, so
+//    the MFMAs of rows the pass does not have are not issued.
+//  * Weights: a wave reads its 32 rows a pair of steps at a time, 128 bytes
+//    (a cache line) per row, 8 rows per instruction -- the pattern HBM serves
+//    at full rate -- two pairs ahead, and passes them through a wave-private
+//    LDS area to the MFMA operand layout. Each lane's 16 bytes (32 nibbles)
+//    of a row per step are widened to f16 with the group scale once and fed
+//    to every row tile: 2 x 4 x RT MFMAs per step.
+// A pass's last row tile may hold rows past the expert's last row: they
+// repeat its last row and are not stored. An expert with more than 64 rows
+// (32 for f32 rows) is done in passes (its weight tile read again).
 // Activations: f16 rows (8-column groups in MFMA order), or f32 rows of X
 // gathered through `rows` and rounded to f16 when staged.
 
@@ -397,6 +409,9 @@ constexpr int kGK = 128;                   // K per step
 constexpr int kGRows = 64;                 // expert rows per pass
 constexpr int kARow = kGK * 2 + 16;        // LDS bytes per activation row (16 B of padding: conflict-free)
 constexpr int kABuf = kGRows * kARow;      // one step's activation tile
+constexpr int kBRow = 128 + 16;            // LDS bytes per weight row of a pair of steps (padded)
+constexpr int kBWave = 32 * kBRow;         // a wave's weight rows
+constexpr int kGemmLds = 2 * kABuf + 4 * kBWave;
 
 template <bool SF16>
 __device__ __forceinline__ uint32_t gscale_bits(const void* s, uint32_t i) {
@@ -410,188 +425,246 @@ __device__ __forceinline__ float gscale_value(uint32_t bits) {
   else return __builtin_bit_cast(float, bits);
 }
 
-struct WeightStep {
-  uint4 w[2];      // 16 bytes of each sub-tile row
-  uint32_t s[2];   // their group scales' bits
-};
+template <int N>
+using IC = std::integral_constant<int, N>;
 
 template <int MODE, bool SF16, bool ROWS32>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
                                           int m1, int nbase, uint8_t* lds) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, q = lane >> 4;
   const uint32_t row_bytes = (uint32_t)a.K / 2, G = (uint32_t)(a.K / a.gs);
-  const int nsteps = a.K / kGK;
-  uint32_t wrow[2];
-  bool wok[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
+  const int nsteps = a.K / kGK, last = nsteps - 1, npairs = (nsteps + 1) / 2, lastp = npairs - 1;
+  // weight row of sub-tile s, row r of it (rows past the matrix: row 0, not stored)
+  auto weight_row = [&](int s, int r, bool* ok) -> uint32_t {
     if (MODE == MODE_GATE_UP) {
-      const int j = nbase + 16 * wave + ln;
-      wok[s] = j < a.I;
-      wrow[s] = (s == 0 ? 0u : (uint32_t)a.I) + (uint32_t)(wok[s] ? j : 0);
+      const int j = nbase + 16 * wave + r;
+      *ok = j < a.I;
+      return (s == 0 ? 0u : (uint32_t)a.I) + (uint32_t)(*ok ? j : 0);
     } else {
-      const int n = nbase + 32 * wave + 16 * s + ln;
-      wok[s] = n < a.N;
-      wrow[s] = (uint32_t)(wok[s] ? n : 0);
-    }
-  }
-  // the lane's 32-column run of step st starts at column 128 st + 32 q; its
-  // group is (4 st + q) / (gs / 32): a step advances it by 4 / (gs / 32) when
-  // that divides, else it is divided out per step
-  const int g32 = a.gs / 32;
-  const bool g_div = 4 % g32 == 0;
-  const uint32_t g_step = g_div ? (uint32_t)(4 / g32) : 0u;
-  const uint32_t wofs[2] = {wrow[0] * row_bytes + 16u * q, wrow[1] * row_bytes + 16u * q};
-  const uint32_t sofs[2] = {wrow[0] * G + (g_div ? (uint32_t)(q / g32) : 0u),
-                            wrow[1] * G + (g_div ? (uint32_t)(q / g32) : 0u)};
-  auto load_w = [&](int st, WeightStep& b) {
-    const uint32_t grp = g_div ? (uint32_t)st * g_step : (uint32_t)((4 * st + q) / g32);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      b.w[s] = stream_load16(Wt + (wofs[s] + (uint32_t)st * (kGK / 2)));
-      b.s[s] = gscale_bits<SF16>(S, sofs[s] + grp);
+      const int n = nbase + 32 * wave + 16 * s + r;
+      *ok = n < a.N;
+      return (uint32_t)(*ok ? n : 0);
     }
   };
-
-  // staging: lane (row 16 wave + lane / 4, 64-byte segment lane % 4) of the tile
-  const int lrow = 16 * wave + (lane >> 2), lseg = lane & 3;
-  uint8_t* const lds_dst = lds + lrow * kARow + lseg * 64;
-
-  for (int mb = m0; mb < m1; mb += kGRows) {
-    const int rows = min(kGRows, m1 - mb), RT = (rows + 15) >> 4;
-    const int am = mb + min(lrow, rows - 1);
-    const int arow = ROWS32 ? (a.rows ? a.rows[am] : am) : am;
-    // a step's slice of this lane's activation row: 64 bytes of f16 (4 x uint4),
-    // or 32 floats (8 x float4); two sets, named by compile-time constants only
-    // (so that they stay in registers)
-    using AVec = std::conditional_t<ROWS32, float4, u32x4>;
-    constexpr int kAV = ROWS32 ? 8 : 4;
-    AVec areg[2][kAV];
-    auto load_a = [&](int st, auto set) {
-      constexpr int R = decltype(set)::value;
-      const AVec* src = reinterpret_cast<const AVec*>(ROWS32 ? (const void*)(a.X + (size_t)arow * a.ldx + st * kGK + 32 * lseg)
-                                                             : (const void*)(a.A + (size_t)arow * a.lda + st * kGK + 32 * lseg));
+  // MFMA layout: lane (ln, q) works on row ln of each sub-tile
+  bool wok[2];
+  uint32_t wrow[2];
 #pragma unroll
-      for (int i = 0; i < kAV; ++i) areg[R][i] = src[i];
-    };
-    auto stage_a = [&](auto set, int buf) {
-      constexpr int R = decltype(set)::value;
-      uint4* dst = reinterpret_cast<uint4*>(lds_dst + buf * kABuf);
-      if constexpr (ROWS32) {
-        // 8 floats -> 8 f16 in MFMA order: position p holds column (p % 2) * 4 + p / 2
+  for (int s = 0; s < 2; ++s) wrow[s] = weight_row(s, ln, &wok[s]);
+  // load layout: load j of a pair reads row 8 j + lane / 8 of the wave's 32
+  // (sub-tile j / 2), bytes 16 (lane % 8) of the pair's 128
+  uint32_t lrowb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bool ok;
+    lrowb[j] = weight_row(j >> 1, 8 * (j & 1) + (lane >> 3), &ok) * row_bytes;
+  }
+  // the lane's 32-column run of step st starts at column 128 st + 32 q; its
+  // group is x / d with x = 4 st + q, d = gs / 32, as the high word of
+  // 2x * ceil(2^31 / d) (the multiplier fits 32 bits for d = 1 too): exact
+  // while x * d < 2^31, i.e. for K below 2^20
+  const uint32_t g32 = (uint32_t)(a.gs / 32), gmul = (uint32_t)((0x80000000ull + g32 - 1) / g32);
+  auto group_of = [&](int st) -> uint32_t { return __umulhi((uint32_t)(8 * st + 2 * q), gmul); };
+  // two pairs in flight: slot B holds pair p with p % 2 == B. The compute of
+  // pair p reads its scales from the slot, so a slot's scales are reloaded
+  // after that compute, its weights before.
+  uint4 breg[2][4];
+  uint32_t sreg[2][2][2];  // [slot][sub-tile][step of the pair]
+  auto load_w = [&](int p, auto slot) {
+    constexpr int B = decltype(slot)::value;
+    // a last pair of one step reads its 64 bytes twice (within the row)
+    const uint32_t cb = 128u * p + 16u * (2 * p + 1 < nsteps ? (lane & 7) : (lane & 3));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) breg[B][j] = stream_load16(Wt + (lrowb[j] + cb));
+  };
+  auto load_s = [&](int p, auto slot) {
+    constexpr int B = decltype(slot)::value;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) sreg[B][s][h] = gscale_bits<SF16>(S, wrow[s] * G + group_of(min(2 * p + h, last)));
+  };
+  uint8_t* const bw = lds + 2 * kABuf + wave * kBWave;
+  auto take_pair = [&](auto slot) {
+    constexpr int B = decltype(slot)::value;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<uint4*>(bw + (8 * j + (lane >> 3)) * kBRow + 16 * (lane & 7)) = breg[B][j];
+    // other lanes of this wave read what it wrote: keep the compiler from
+    // moving the reads above the writes (LDS serves a wave in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  const uint32_t c0 = widen_c0(xor4), c1 = widen_c1(xor4);
+  const int srow = tid >> 4, aseg = tid & 15;  // staging: row 16 i + srow, 16 bytes at 16 aseg
+
+  // f32 rows take twice the registers per staged row: passes of 32 rows
+  constexpr int kPassRows = ROWS32 ? 32 : kGRows;
+  for (int mb = m0; mb < m1; mb += kPassRows) {
+    const int rows = min(kPassRows, m1 - mb);
+    auto pass = [&](auto rt_c) {
+      constexpr int RT = decltype(rt_c)::value;
+      int arow[RT];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        const int am = mb + min(16 * i + srow, rows - 1);
+        arow[i] = ROWS32 ? (a.rows ? a.rows[am] : am) : am;
+      }
+      // a step's share of the tile: RT x 16 bytes of f16, or RT x 8 floats;
+      // two sets, named by compile-time constants only (so that they stay in
+      // registers)
+      using AVec = std::conditional_t<ROWS32, float4, u32x4>;
+      constexpr int kAV = ROWS32 ? 2 * RT : RT;
+      AVec areg[2][kAV];
+      auto load_a = [&](int st, auto set) {
+        constexpr int R = decltype(set)::value;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          if constexpr (ROWS32) {
+            const float4* src = reinterpret_cast<const float4*>(a.X + (size_t)arow[i] * a.ldx + st * kGK + 8 * aseg);
+            areg[R][2 * i] = src[0];
+            areg[R][2 * i + 1] = src[1];
+          } else {
+            areg[R][i] = *reinterpret_cast<const u32x4*>(a.A + (size_t)arow[i] * a.lda + st * kGK + 8 * aseg);
+          }
+        }
+      };
+      auto stage_a = [&](auto set, int buf) {
+        constexpr int R = decltype(set)::value;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          uint8_t* dst = lds + buf * kABuf + (16 * i + srow) * kARow + 16 * aseg;
+          if constexpr (ROWS32) {
+            // 8 floats -> 8 f16 in MFMA order: position p holds column (p % 2) * 4 + p / 2
+            const float4 lo = areg[R][2 * i], hi = areg[R][2 * i + 1];
+            const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            half8 h;
+#pragma unroll
+            for (int p = 0; p < 8; ++p) h[p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
+            *reinterpret_cast<half8*>(dst) = h;
+          } else {
+            *reinterpret_cast<u32x4*>(dst) = areg[R][i];
+          }
+        }
+      };
+
+      f32x4 acc[RT][2];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) acc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+      // step h of the current pair, activations from LDS buffer buf; the
+      // fragments of slice i + 1 are read while slice i is widened and multiplied
+      auto compute = [&](int h, int buf, auto slot) {
+        constexpr int B = decltype(slot)::value;
+        const uint8_t* A = lds + buf * kABuf + ln * kARow + 64 * q;
+        uint4 w[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) w[s] = *reinterpret_cast<const uint4*>(bw + (16 * s + ln) * kBRow + 64 * h + 16 * q);
+        half8 av[2][RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) av[0][rt] = *reinterpret_cast<const half8*>(A + rt * 16 * kARow);
+        __half2 s2[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) s2[s] = __float2half2_rn(gscale_value<SF16>(sreg[B][s][h]));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float4 lo = areg[R][2 * i], hi = areg[R][2 * i + 1];
-          const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-          half8 h;
+          if (i < 3) {
 #pragma unroll
-          for (int p = 0; p < 8; ++p) h[p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
-          dst[i] = __builtin_bit_cast(uint4, h);
+            for (int rt = 0; rt < RT; ++rt)
+              av[(i + 1) & 1][rt] = *reinterpret_cast<const half8*>(A + rt * 16 * kARow + 16 * (i + 1));
+          }
+          const uint32_t w0 = i == 0 ? w[0].x : i == 1 ? w[0].y : i == 2 ? w[0].z : w[0].w;
+          const uint32_t w1 = i == 0 ? w[1].x : i == 1 ? w[1].y : i == 2 ? w[1].z : w[1].w;
+          const half8 b0 = widen8(w0, s2[0], c0, c1), b1 = widen8(w1, s2[1], c0, c1);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            acc[rt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i & 1][rt], b0, acc[rt][0], 0, 0, 0);
+            acc[rt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i & 1][rt], b1, acc[rt][1], 0, 0, 0);
+          }
         }
+      };
+
+      // Pair p: its weights (slot B) and both of its steps' activation tiles
+      // go to LDS first; then the next pair's activations and the weights of
+      // pair p + 2 are issued, both steps computed, and the scales of pair
+      // p + 2 issued. Loads return in issue order for the wait counts, so
+      // each wait here is for loads older than the last weights issued: two
+      // pairs stay in flight while a pair is computed. Every load is
+      // unconditional (indices past the end repeat the last pair or step, in
+      // L2), so the compiler's wait counts stay exact.
+      auto body = [&](int p, auto slot, bool more) {
+        __syncthreads();  // every wave is done with the previous pair's tiles
+        take_pair(slot);
+        stage_a(IC<0>{}, 0);
+        stage_a(IC<1>{}, 1);
+        __syncthreads();
+        if (more) {
+          load_a(min(2 * p + 2, last), IC<0>{});
+          load_a(min(2 * p + 3, last), IC<1>{});
+          load_w(min(p + 2, lastp), slot);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0, 0, slot);
+        if (2 * p + 1 < nsteps) compute(1, 1, slot);
+        if (more) load_s(min(p + 2, lastp), slot);
+      };
+
+      // the same issue order as the loop's (weights and scales of a slot, the
+      // activations, the other slot): the compiler's wait counts at the loop
+      // head merge the prologue's order with the loop's
+      load_w(0, IC<0>{});
+      load_s(0, IC<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_a(0, IC<0>{});
+      load_a(min(1, last), IC<1>{});
+      load_w(min(1, lastp), IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_s(min(1, lastp), IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      int p = 0;
+      for (; p + 2 < npairs; p += 2) {
+        body(p, IC<0>{}, true);
+        body(p + 1, IC<1>{}, true);
+      }
+      if (p + 2 == npairs) {
+        body(p, IC<0>{}, true);
+        body(p + 1, IC<1>{}, false);
       } else {
-        u32x4* d = reinterpret_cast<u32x4*>(dst);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = areg[R][i];
+        body(p, IC<0>{}, false);
       }
-    };
 
-    f32x4 acc[4][2];
+      // D layout: lane (ln, q) holds rows 4q .. 4q+3 of column ln of each 16x16 tile
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+      for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) acc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto compute = [&](const WeightStep& b, int buf) {
-      const uint8_t* A = lds + buf * kABuf + ln * kARow + 64 * q;
-      __half2 s2[2];
-      uint32_t wd[2][4];
+        for (int j = 0; j < 4; ++j) {
+          const int m = mb + 16 * rt + 4 * q + j;
+          if (m >= m1) continue;
+          if (MODE == MODE_GATE_UP) {
+            if (wok[0])
+              a.act[(size_t)m * a.ldact + perm_pos(nbase + 16 * wave + ln)] =
+                  (_Float16)(silu(acc[rt][0][j]) * acc[rt][1][j]);
+          } else {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        s2[s] = __float2half2_rn(gscale_value<SF16>(b.s[s]));
-        wd[s][0] = b.w[s].x ^ xor4;
-        wd[s][1] = b.w[s].y ^ xor4;
-        wd[s][2] = b.w[s].z ^ xor4;
-        wd[s][3] = b.w[s].w ^ xor4;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half8 b0 = widen8(wd[0][i], s2[0]), b1 = widen8(wd[1][i], s2[1]);
-        // all four row tiles every step, also past the pass's rows (those
-        // repeat its last row and are not stored): no branch between the
-        // accumulators' updates
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          const half8 av = *reinterpret_cast<const half8*>(A + rt * 16 * kARow + 16 * i);
-          acc[rt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[rt][0], 0, 0, 0);
-          acc[rt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[rt][1], 0, 0, 0);
+            for (int s = 0; s < 2; ++s)
+              if (wok[s]) a.Y[(size_t)m * a.ldy + nbase + 32 * wave + 16 * s + ln] = acc[rt][s][j];
+          }
         }
       }
     };
-
-    // Activations are loaded two steps ahead (register sets a0 / a1) and
-    // staged at the end of the step before their use; weights one step ahead.
-    // The steady state has unconditional loads (the compiler's wait counts
-    // then keep them in flight), the last one to three steps follow.
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    WeightStep b0, b1;
-    load_a(0, S0{});
-    load_a(nsteps > 1 ? 1 : 0, S1{});
-    load_w(0, b0);
-    stage_a(S0{}, 0);
-    __syncthreads();
-    int st = 0;
-    for (; st + 3 < nsteps; st += 2) {
-      load_a(st + 2, S0{});
-      load_w(st + 1, b1);
-      compute(b0, 0);
-      stage_a(S1{}, 1);
-      __syncthreads();
-      load_a(st + 3, S1{});
-      load_w(st + 2, b0);
-      compute(b1, 1);
-      stage_a(S0{}, 0);
-      __syncthreads();
-    }
-    const int left = nsteps - st;  // 1, 2 or 3
-    if (left == 3) {
-      load_a(st + 2, S0{});
-      load_w(st + 1, b1);
-      compute(b0, 0);
-      stage_a(S1{}, 1);
-      __syncthreads();
-      load_w(st + 2, b0);
-      compute(b1, 1);
-      stage_a(S0{}, 0);
-      __syncthreads();
-      compute(b0, 0);
-    } else if (left == 2) {
-      load_w(st + 1, b1);
-      compute(b0, 0);
-      stage_a(S1{}, 1);
-      __syncthreads();
-      compute(b1, 1);
+    // the same on every thread of the workgroup: no thread skips a barrier
+    if constexpr (ROWS32) {
+      if (rows <= 16) pass(IC<1>{});
+      else pass(IC<2>{});
     } else {
-      compute(b0, 0);
-    }
-
-    // D layout: lane (ln, q) holds rows 4q .. 4q+3 of column ln of each 16x16 tile
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      if (rt >= RT) break;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = mb + 16 * rt + 4 * q + j;
-        if (m >= m1) continue;
-        if (MODE == MODE_GATE_UP) {
-          if (wok[0])
-            a.act[(size_t)m * a.ldact + perm_pos(nbase + 16 * wave + ln)] =
-                (_Float16)(silu(acc[rt][0][j]) * acc[rt][1][j]);
-        } else {
-#pragma unroll
-          for (int s = 0; s < 2; ++s)
-            if (wok[s]) a.Y[(size_t)m * a.ldy + nbase + 32 * wave + 16 * s + ln] = acc[rt][s][j];
-        }
+      switch ((rows + 15) >> 4) {
+        case 1: pass(IC<1>{}); break;
+        case 2: pass(IC<2>{}); break;
+        case 3: pass(IC<3>{}); break;
+        default: pass(IC<4>{}); break;
       }
     }
     __syncthreads();  // the LDS tiles are refilled by the next pass
@@ -599,8 +672,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
 }
 
 template <int MODE, bool ROWS32>
-__global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kABuf];
+__global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   // all column tiles of one expert on one XCD: its activation rows stay in that L2
   const int L = xcd_contiguous(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
   const int e = L / gridDim.x, tile = L % gridDim.x;
