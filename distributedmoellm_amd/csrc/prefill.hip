@@ -411,7 +411,9 @@ constexpr int kARow = kGK * 2 + 16;        // LDS bytes per activation row (16 B
 constexpr int kABuf = kGRows * kARow;      // one step's activation tile
 constexpr int kBRow = 128 + 16;            // LDS bytes per weight row of a pair of steps (padded)
 constexpr int kBWave = 32 * kBRow;         // a wave's weight rows
-constexpr int kGemmLds = 2 * kABuf + 4 * kBWave;
+constexpr int kSRow = 144;                 // LDS bytes per row of a wave's scale window (16-byte aligned)
+constexpr int kSWave = 32 * kSRow;         // a wave's scale rows
+constexpr int kGemmLds = 2 * kABuf + 4 * kBWave + 4 * kSWave;
 
 template <bool SF16>
 __device__ __forceinline__ uint32_t gscale_bits(const void* s, uint32_t i) {
@@ -428,7 +430,9 @@ __device__ __forceinline__ float gscale_value(uint32_t bits) {
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-template <int MODE, bool SF16, bool ROWS32>
+// SWIN: the rows' scales (at most 128 bytes a row, 16-byte aligned) are read
+// once per tile into a wave-private LDS window instead of per pair from HBM
+template <int MODE, bool SF16, bool ROWS32, bool SWIN>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
                                           int m1, int nbase, uint8_t* lds) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, q = lane >> 4;
@@ -478,12 +482,31 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
     for (int j = 0; j < 4; ++j) breg[B][j] = stream_load16(Wt + (lrowb[j] + cb));
   };
   auto load_s = [&](int p, auto slot) {
-    constexpr int B = decltype(slot)::value;
+    if constexpr (!SWIN) {
+      constexpr int B = decltype(slot)::value;
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) sreg[B][s][h] = gscale_bits<SF16>(S, wrow[s] * G + group_of(min(2 * p + h, last)));
+        for (int h = 0; h < 2; ++h) sreg[B][s][h] = gscale_bits<SF16>(S, wrow[s] * G + group_of(min(2 * p + h, last)));
+    }
   };
+  // the scale window: row r of the wave's 32 at r * kSRow, its scales as stored
+  uint8_t* const swin = lds + 2 * kABuf + 4 * kBWave + wave * kSWave;
+  if constexpr (SWIN) {
+    // load j: row 8 j + lane / 8 (as the weights), bytes 16 (lane % 8) of the
+    // row's scales; lanes past the row's end read its start (not used)
+    const uint32_t sb = SF16 ? 2u : 4u, srow_bytes = G * sb;
+    const uint32_t b = 16u * (lane & 7) < srow_bytes ? 16u * (lane & 7) : 0u;
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = *gptr<u32x4>(static_cast<const uint8_t*>(S) + (lrowb[j] / row_bytes) * srow_bytes + b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(swin + (8 * j + (lane >> 3)) * kSRow + b) = v[j];
+    // read by this wave's lanes only (LDS serves a wave in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
   uint8_t* const bw = lds + 2 * kABuf + wave * kBWave;
   auto take_pair = [&](auto slot) {
     constexpr int B = decltype(slot)::value;
@@ -557,7 +580,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
 
       // step h of the current pair, activations from LDS buffer buf; the
       // fragments of slice i + 1 are read while slice i is widened and multiplied
-      auto compute = [&](int h, int buf, auto slot) {
+      auto compute = [&](int h, int buf, auto slot, int p_cur) {
         constexpr int B = decltype(slot)::value;
         const uint8_t* A = lds + buf * kABuf + ln * kARow + 64 * q;
         uint4 w[2];
@@ -568,7 +591,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
         for (int rt = 0; rt < RT; ++rt) av[0][rt] = *reinterpret_cast<const half8*>(A + rt * 16 * kARow);
         __half2 s2[2];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) s2[s] = __float2half2_rn(gscale_value<SF16>(sreg[B][s][h]));
+        for (int s = 0; s < 2; ++s) {
+          uint32_t bits;
+          if constexpr (SWIN) {
+            const uint8_t* sp = swin + (16 * s + ln) * kSRow + group_of(2 * (p_cur) + h) * (SF16 ? 2 : 4);
+            if constexpr (SF16) bits = *reinterpret_cast<const uint16_t*>(sp);
+            else bits = *reinterpret_cast<const uint32_t*>(sp);
+          } else {
+            bits = sreg[B][s][h];
+          }
+          s2[s] = __float2half2_rn(gscale_value<SF16>(bits));
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if (i < 3) {
@@ -607,8 +640,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
           load_w(min(p + 2, lastp), slot);
         }
         __builtin_amdgcn_sched_barrier(0);
-        compute(0, 0, slot);
-        if (2 * p + 1 < nsteps) compute(1, 1, slot);
+        compute(0, 0, slot, p);
+        if (2 * p + 1 < nsteps) compute(1, 1, slot, p);
         if (more) load_s(min(p + 2, lastp), slot);
       };
 
@@ -684,8 +717,16 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   const uint8_t* Wt = a.which ? d.dn_w : d.gu_w;
   const void* S = a.which ? d.dn_s : d.gu_s;
   const uint32_t xor4 = d.xor8 * 0x01010101u;
-  if (d.s_f16) gemm_tile<MODE, true, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, lds);
-  else gemm_tile<MODE, false, ROWS32>(a, Wt, S, xor4, m0, m1, nbase, lds);
+  // scale rows of at most 128 bytes, 16-byte aligned: read once into LDS
+  const uint32_t srow_bytes = (uint32_t)(a.K / a.gs) * (d.s_f16 ? 2u : 4u);
+  const bool swin = srow_bytes <= 128 && srow_bytes % 16 == 0 && ((uintptr_t)S & 15) == 0;
+  if (d.s_f16) {
+    if (swin) gemm_tile<MODE, true, ROWS32, true>(a, Wt, S, xor4, m0, m1, nbase, lds);
+    else gemm_tile<MODE, true, ROWS32, false>(a, Wt, S, xor4, m0, m1, nbase, lds);
+  } else {
+    if (swin) gemm_tile<MODE, false, ROWS32, true>(a, Wt, S, xor4, m0, m1, nbase, lds);
+    else gemm_tile<MODE, false, ROWS32, false>(a, Wt, S, xor4, m0, m1, nbase, lds);
+  }
 }
 
 // ------------------------------------------------------------------ combine
