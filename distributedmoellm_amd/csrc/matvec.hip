@@ -554,7 +554,7 @@ static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr,
       const int v = e ? atoi(e) : 0;
       return v >= 1 && v <= 64 ? v : 0;
     }();
-    const int ng_max = ng_env ? ng_env : (job.half_in > 0 ? 32 : 8);
+    const int ng_max = ng_env ? ng_env : (job.half_in > 0 ? 32 : 16);
     int ng = (int)(groups / 2048);
     ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
     const int wave_rows = ng * G * rpp;
