@@ -208,6 +208,58 @@ def decode384(args, L, per_layer=False):
     return res
 
 
+def decode384_gs64(args, L):
+    """The 384 evaluations per step at groups of 64 through the whole layer
+    call (moe_q4_layer_i8: int8 activations, as moelan's _moe_q4i; and
+    moe_q4_layer: float activations), each timed per call with HIP events on
+    the stream the call launches on."""
+    import torch
+    H, I, gs, npool, per_step = 2048, 768, 64, 1024, 384
+    pool = Int4Pool(npool, H, I, gs, seed=3)
+    rng = np.random.default_rng(4)
+    nvar = 8
+    calls = Calls([(np.sort(rng.choice(npool, per_step, replace=False)).astype(np.int32),
+                    [np.zeros(1, np.int32) for _ in range(per_step)],
+                    [rng.random(1).astype(np.float32) for _ in range(per_step)]) for _ in range(nvar)])
+    x = torch.randn((1, H), device="cuda")
+    out = torch.zeros((1, H), device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    step_bytes = per_step * pool.expert_bytes + 2 * H * 4
+    res = {}
+    for name, fn, need in (("int8_act", L.moe_q4_layer_i8, L.moe_q4_layer_i8_workspace(per_step, H, I, gs)),
+                           ("float_act", L.moe_q4_layer, L.moe_q4_layer_workspace(per_step, H, I))):
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+
+        def call(c):
+            rc = fn(x.data_ptr(), H, pool.table.data_ptr(), c["eidx"], c["k"], c["poff"], c["prow"], c["pw"],
+                    c["P"], c["rrow"], c["rptr"], c["rpair"], c["nr"], out.data_ptr(), H, H, I, gs,
+                    c["max_rows"], ws.data_ptr(), need, stream)
+            if rc:
+                from distributedmoellm_amd import _lib
+                raise RuntimeError(_lib.last_error())
+        for i in range(args.warmup):
+            call(calls.items[i % nvar])
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(args.steps):
+            call(calls.items[i % nvar])
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        res[name] = dict(ms_per_step=ms, gbs=step_bytes / (ms / 1e3) / 1e9,
+                         hbm_frac=step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS)
+        log(f"decode384 gs=64 {name}: {ms * 1e3:.1f} us/step, {res[name]['gbs']:.0f} GB/s")
+        del ws
+    res["bytes_per_step"] = step_bytes
+    res["workload"] = ("one token's 384 expert evaluations per layer call, H=2048 I=768, int4 group 64, "
+                       "f16 scales, 1024-expert pool; whole call (rounding, gate|up, down, combine)")
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline_decode(seconds: float = 12.0):
     """The reference's fused layer kernel restated in C/OpenMP (oracle/cpuref.c)
     on the host cores: one token's 384 experts per call from a pool of 64
@@ -400,7 +452,7 @@ def main() -> int:
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, prefill, copy "
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, prefill, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -424,6 +476,8 @@ def main() -> int:
             res["decode"] = r
         if "prefill" in only:
             res["prefill"] = prefill_c4(args, L)
+        if "decode_i8" in only:
+            res["decode_i8"] = decode384_gs64(args, L)
         if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
             import torch
             a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -443,6 +497,7 @@ def main() -> int:
     extras = {}
     if "per_layer_calls" in r:
         extras["per_layer_calls"] = r.pop("per_layer_calls")
+    extras["decode384_gs64"] = decode384_gs64(args, L)
     if args.stack:
         extras["stack_235b"] = stack_decode(args, L)
     log("prefill (Qwen3-30B-A3B layer, T=512) ...")

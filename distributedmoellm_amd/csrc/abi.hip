@@ -219,6 +219,69 @@ MOE_API int moe_q4_layer(const float* x, int ldx, const moe_q4_expert* table, co
   return run_q4_layer(a, as_stream(stream));
 }
 
+static int check_i8_shape(const char* who, int H, int I, int gs) {
+  REQUIRE(H > 0 && I > 0 && gs > 0, "%s: H=%d, I=%d and gs=%d must be positive", who, H, I, gs);
+  if (gs % 64 != 0 || gs > 512 || H % gs != 0 || I % gs != 0)
+    return set_error(MOE_EUNSUPPORTED, "%s: group size %d must be a multiple of 64 up to 512 dividing H=%d and I=%d",
+                     who, gs, H, I);
+  return MOE_OK;
+}
+
+MOE_API size_t moe_q4_layer_i8_workspace(int P, int H, int I, int gs) {
+  if (P <= 0 || H <= 0 || I <= 0 || gs <= 0 || H % gs || I % gs) return 0;
+  return q4i8_layer_workspace(P, H, I, gs);
+}
+
+MOE_API int moe_q4_layer_i8(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k,
+                            const int* poff, const int* prow, const float* pw, int P, const int* rrow, const int* rptr,
+                            const int* rpair, int nr, float* out, int ldo, int H, int I, int gs, int max_rows,
+                            void* workspace, size_t ws_bytes, void* stream) {
+  if (int rc = check_i8_shape("moe_q4_layer_i8", H, I, gs)) return rc;
+  REQUIRE(k >= 0 && P >= 0 && nr >= 0, "moe_q4_layer_i8: k=%d P=%d nr=%d", k, P, nr);
+  if (k == 0 || P == 0) return MOE_OK;
+  REQUIRE(max_rows > 0 && max_rows <= P, "moe_q4_layer_i8: max_rows=%d for P=%d", max_rows, P);
+  REQUIRE(ldx >= H && ldo >= H, "moe_q4_layer_i8: ldx=%d ldo=%d must be >= H=%d", ldx, ldo, H);
+  REQUIRE(x && table && poff && prow && pw && rrow && rptr && rpair && out, "moe_q4_layer_i8: null pointer");
+  const size_t need = q4i8_layer_workspace(P, H, I, gs);
+  if (workspace == nullptr || ws_bytes < need)
+    return set_error(MOE_EWORKSPACE, "moe_q4_layer_i8: workspace of %zu bytes, %zu needed", ws_bytes, need);
+  REQUIRE(aligned(workspace, 256), "moe_q4_layer_i8: workspace must be 256-byte aligned");
+  Q4LayerArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.table = reinterpret_cast<const ExpertDesc*>(table);
+  a.eidx = eidx;
+  a.k = k;
+  a.poff = poff;
+  a.prow = prow;
+  a.pw = pw;
+  a.P = P;
+  a.rrow = rrow;
+  a.rptr = rptr;
+  a.rpair = rpair;
+  a.nr = nr;
+  a.out = out;
+  a.ldo = ldo;
+  a.H = H;
+  a.I = I;
+  a.gs = gs;
+  a.max_rows = max_rows;
+  a.workspace = workspace;
+  return run_q4i8_layer(a, as_stream(stream));
+}
+
+MOE_API int moe_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int gs, int8_t* q, float* d,
+                         int32_t* s8, void* stream) {
+  REQUIRE(n >= 0 && K > 0 && gs > 0, "moe_round_q8: n=%d K=%d gs=%d", n, K, gs);
+  if (gs % 64 != 0 || gs > 512 || K % gs != 0)
+    return set_error(MOE_EUNSUPPORTED, "moe_round_q8: group size %d must be a multiple of 64 up to 512 dividing K=%d",
+                     gs, K);
+  if (n == 0) return MOE_OK;
+  REQUIRE(ldx >= K, "moe_round_q8: ldx=%d must be >= K=%d", ldx, K);
+  REQUIRE(x && q && d && s8, "moe_round_q8: null pointer");
+  return run_round_q8(x, ldx, xrow, n, K, 0, gs, q, d, s8, as_stream(stream));
+}
+
 MOE_API int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, void* stream) {
   REQUIRE(n >= 0 && I > 0 && ldh >= 2 * I && lda >= I, "moe_silu_mul: n=%d I=%d ldh=%d lda=%d", n, I, ldh, lda);
   if (n == 0) return MOE_OK;

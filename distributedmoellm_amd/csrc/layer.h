@@ -26,6 +26,9 @@ struct Q4LayerArgs {
 
 size_t q4_layer_workspace(int P, int H, int I);
 int run_q4_layer(const Q4LayerArgs& a, hipStream_t st);
+// the same call with activations rounded to int8 per group (gs a multiple of 64)
+size_t q4i8_layer_workspace(int P, int H, int I, int gs);
+int run_q4i8_layer(const Q4LayerArgs& a, hipStream_t st);
 int run_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, hipStream_t st);
 int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
                 float* out, int ldo, int H, hipStream_t st);

@@ -218,6 +218,82 @@ int run_q4_layer(const Q4LayerArgs& a, hipStream_t st) {
   return run_combine_runs(y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st);
 }
 
+// The workspace of the int8-activation call, each piece 256-byte aligned:
+// h [P, 2I] f32, y [P, H] f32, the rounded inputs [P, H] bytes with d, s8
+// [P, H/gs], the rounded SiLU outputs [P, I] bytes with d, s8 [P, I/gs].
+struct Q4I8Space {
+  float* h;
+  float* y;
+  int8_t* qx;
+  float* dx;
+  int* sx;
+  int8_t* qa;
+  float* da;
+  int* sa;
+  size_t bytes;
+};
+
+static Q4I8Space q4i8_layout(void* base, int P, int H, int I, int gs) {
+  Q4I8Space w{};
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off += (n + 255) / 256 * 256;
+    return (char*)base + o;
+  };
+  const size_t p = (size_t)P;
+  w.h = (float*)take(p * 2 * I * 4);
+  w.y = (float*)take(p * H * 4);
+  w.qx = (int8_t*)take(p * H);
+  w.dx = (float*)take(p * (H / gs) * 4);
+  w.sx = (int*)take(p * (H / gs) * 4);
+  w.qa = (int8_t*)take(p * I);
+  w.da = (float*)take(p * (I / gs) * 4);
+  w.sa = (int*)take(p * (I / gs) * 4);
+  w.bytes = off;
+  return w;
+}
+
+size_t q4i8_layer_workspace(int P, int H, int I, int gs) { return q4i8_layout(nullptr, P, H, I, gs).bytes; }
+
+// _moe_q4i (moelan/kernels.py:854-917): round the pairs' input rows, gate|up,
+// SiLU * up rounded again, down, then the same weighted combine as the float call
+int run_q4i8_layer(const Q4LayerArgs& a, hipStream_t st) {
+  const Q4I8Space w = q4i8_layout(a.workspace, a.P, a.H, a.I, a.gs);
+  MVShape s1, s2;
+  plan_matvec(FMT_Q4, 2 * a.I, a.H, a.gs, &s1);
+  plan_matvec(FMT_Q4, a.H, a.I, a.gs, &s2);
+  int rc = run_round_q8(a.x, a.ldx, a.prow, a.P, a.H, 0, a.gs, w.qx, w.dx, w.sx, st);
+  if (rc) return rc;
+
+  MVJob j1{};
+  j1.y = w.h;
+  j1.ldy = 2 * a.I;
+  j1.seg = a.poff;
+  j1.n = a.P;
+  j1.experts = a.table;
+  j1.eidx = a.eidx;
+  j1.which = 0;
+  rc = run_matvec_q4i8(s1, j1, a.k, w.qx, w.dx, w.sx, st);
+  if (rc) return rc;
+
+  rc = run_round_q8(w.h, 2 * a.I, nullptr, a.P, a.I, a.I, a.gs, w.qa, w.da, w.sa, st);
+  if (rc) return rc;
+
+  MVJob j2{};
+  j2.y = w.y;
+  j2.ldy = a.H;
+  j2.seg = a.poff;
+  j2.n = a.P;
+  j2.experts = a.table;
+  j2.eidx = a.eidx;
+  j2.which = 1;
+  rc = run_matvec_q4i8(s2, j2, a.k, w.qa, w.da, w.sa, st);
+  if (rc) return rc;
+
+  return run_combine_runs(w.y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st);
+}
+
 }  // namespace moe
 
 namespace moe {

@@ -49,6 +49,15 @@ struct MVJob {
 };
 
 int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh);
+// rows xrow[p] (or p) of x, or silu(h[:, :half]) * h[:, half:] when half > 0,
+// rounded to int8 per group of gs (a multiple of 64 up to 512): q [n, K] bytes,
+// each 32-column chunk as its 16 even columns then its 16 odd ones; d, s8 [n, K/gs]
+int run_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int half, int gs, int8_t* q, float* d, int* s8,
+                 hipStream_t st);
+// y[pair] = int8 row `pair` of q (with its d, s8) against W_m, for every int4
+// matrix m and its pairs (job.seg; job.x and job.xrow are not used)
+int run_matvec_q4i8(const MVShape& sh, const MVJob& job, int nmat, const int8_t* q, const float* dq, const int* s8q,
+                    hipStream_t st);
 // y[pair] = x[xrow[pair]] @ W_m.T for every matrix m and its pairs
 int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st);
 

@@ -475,6 +475,219 @@ __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
   }
 }
 
+// ------------------------------------------------------------------ int8 activations
+//
+// The reference's int8-activation layer call (_moe_q4i, moelan/kernels.py:
+// 854-917): each row of activations is rounded to int8 per group of gs
+// (a multiple of 64) by _round_q8 (:833-852); a group's product with int4
+// weights is an exact integer sum of unsigned nibble * int8 (_q4c64,
+// :807-831), turned into f32 once: f32(isum - 8 * sum q) * (s_w * d).
+// Rounded rows are stored per 32-column chunk as the 16 even columns' bytes
+// then the 16 odd ones', so that one nibble dword meets its activations in
+// two v_dot4_i32_i8: low nibbles with the even bytes, high with the odd.
+
+// One wave per (row, group): the group's largest |v|, the scale m / 127 (1 if
+// m is 0), q = floor(v * (1 / scale) + 0.5) with the product and the sum
+// rounded separately, as the reference writes them. PER = gs / 64 values a lane.
+template <int PER>
+__global__ __launch_bounds__(256) void round_q8_kernel(const float* x, int ldx, const int* xrow, int n, int K, int half,
+                                                       int gs, int8_t* q, float* d, int* s8) {
+  const int G = K / gs;
+  const long wid = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wid >= (long)n * G) return;  // the whole wave: no barrier below
+  const int p = (int)(wid / G), g = (int)(wid % G);
+  const float* row = x + (size_t)(xrow ? xrow[p] : p) * ldx;
+  float v[PER];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int c = g * gs + 64 * i + lane;
+    float t = row[c];
+    if (half > 0) t = silu(t) * row[half + c];
+    v[i] = t;
+    m = fmaxf(m, fabsf(t));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const float sc = m > 0.f ? m / 127.0f : 1.0f;
+  const float inv = 1.0f / sc;
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int qi = (int)floorf(__fadd_rn(__fmul_rn(v[i], inv), 0.5f));
+    sum += qi;
+    const int c = g * gs + 64 * i + lane, k = c & 31;
+    q[(size_t)p * K + (c - k) + (k & 1) * 16 + (k >> 1)] = (int8_t)qi;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  if (lane == 0) {
+    d[(size_t)p * G + g] = sc;
+    s8[(size_t)p * G + g] = 8 * sum;
+  }
+}
+
+// the sum over aligned groups of GD lanes (GD = 2, 4), in every lane of the group
+template <int GD>
+__device__ __forceinline__ int lane_group_isum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);  // quad_perm [1,0,3,2]
+  if constexpr (GD >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);  // quad_perm [2,3,0,1]
+  return v;
+}
+
+// As mv_fast_body (L lanes per row, CPL chunks per lane, two register buffers
+// of G passes) with int8 activations: per chunk two v_dot4 per nibble dword,
+// the group's integer sum gathered over its GD lanes, and one f32 term per group
+// added by the group's last lane.
+template <int L, int CPL, int GD, bool SF16>
+__device__ __forceinline__ void mv_q4i8_body(const MVShape& sh, const MVJob& job, const MatRef& M, const int8_t* q,
+                                             const float* dq, const int* s8q, int A, int ng, int p0, int p1,
+                                             int row_begin) {
+  constexpr int G = CPL >= 2 ? 2 : 4;
+  constexpr int RPP = 64 / L;
+  const int lane = threadIdx.x & 63;
+  const int lg = lane / L, lc = lane % L;
+  const bool active = lc < A;
+  const int gx = sh.I / sh.gs;  // groups of an activation row
+  uint32_t woff[CPL], soff[CPL];
+  bool tail[CPL];  // the chunk is its group's last: its lane adds the group's term
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int chunk = active ? lc + c * A : 0;
+    woff[c] = (uint32_t)chunk * 16u;
+    soff[c] = (uint32_t)(chunk / GD);
+    tail[c] = active && (chunk % GD) == GD - 1;
+  }
+  const uint32_t omax = (uint32_t)sh.O - 1u, rb = (uint32_t)sh.row_bytes, gpr = (uint32_t)sh.G;
+  const uint8_t* const W = M.w;
+  const void* const S = M.s;
+
+  for (int p = p0; p < p1; ++p) {
+    uint32_t xe[CPL][4], xo[CPL][4];
+    float dx[CPL];
+    int sx[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int chunk = active ? lc + c * A : 0;
+      const uint4 e = *reinterpret_cast<const uint4*>(q + (size_t)p * sh.I + 32 * chunk);
+      const uint4 o = *reinterpret_cast<const uint4*>(q + (size_t)p * sh.I + 32 * chunk + 16);
+      xe[c][0] = e.x; xe[c][1] = e.y; xe[c][2] = e.z; xe[c][3] = e.w;
+      xo[c][0] = o.x; xo[c][1] = o.y; xo[c][2] = o.z; xo[c][3] = o.w;
+      dx[c] = dq[(size_t)p * gx + chunk / GD];
+      sx[c] = s8q[(size_t)p * gx + chunk / GD];
+    }
+    uint4 wb[2][G][CPL];
+    uint32_t sb[2][G][CPL];
+    auto issue = [&](auto buf, int grp) {
+      constexpr int B = decltype(buf)::value;
+      const uint32_t obase = (uint32_t)(row_begin + grp * (G * RPP) + lg);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t o = min(obase + (uint32_t)(g * RPP), omax);
+        const uint32_t wrow = __umul24(o, rb), srow = __umul24(o, gpr);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          wb[B][g][c] = stream_load16(W + (wrow + woff[c]));
+          sb[B][g][c] = sload_bits<SF16>(S, srow + soff[c]);
+        }
+      }
+    };
+    auto compute = [&](auto buf, int grp) {
+      constexpr int B = decltype(buf)::value;
+      const int obase = row_begin + grp * (G * RPP) + lg;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float a = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const uint32_t w[4] = {wb[B][g][c].x ^ M.xor4, wb[B][g][c].y ^ M.xor4, wb[B][g][c].z ^ M.xor4,
+                                 wb[B][g][c].w ^ M.xor4};
+          int isum = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            isum = __builtin_amdgcn_sdot4((int)(w[i] & 0x0F0F0F0Fu), (int)xe[c][i], isum, false);
+            isum = __builtin_amdgcn_sdot4((int)((w[i] >> 4) & 0x0F0F0F0Fu), (int)xo[c][i], isum, false);
+          }
+          isum = lane_group_isum<GD>(isum);
+          if (tail[c]) a += (float)(isum - sx[c]) * (scale_value<SF16>(sb[B][g][c]) * dx[c]);
+        }
+        const float acc = lane_group_sum<L>(a);
+        const int o = obase + g * RPP;
+        if (lc == L - 1 && o < sh.O) job.y[(size_t)p * job.ldy + o] = acc;
+      }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    issue(B0{}, 0);
+    int grp = 0;
+    for (; grp + 2 < ng; grp += 2) {
+      issue(B1{}, grp + 1);
+      compute(B0{}, grp);
+      issue(B0{}, grp + 2);
+      compute(B1{}, grp + 1);
+    }
+    if (grp + 1 < ng) {
+      issue(B1{}, grp + 1);
+      compute(B0{}, grp);
+      compute(B1{}, grp + 1);
+    } else {
+      compute(B0{}, grp);
+    }
+  }
+}
+
+template <int L, int CPL, int GD>
+__global__ __launch_bounds__(256) void mv_q4i8_kernel(MVShape sh, MVJob job, const int8_t* q, const float* dq,
+                                                      const int* s8q, int A, int ng) {
+  constexpr int G = CPL >= 2 ? 2 : 4;
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  if (p0 >= p1) return;
+  const int wave = threadIdx.x >> 6;
+  const int wave_rows = ng * G * (64 / L);
+  const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * wave_rows;
+  if (row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
+  const MatRef M = resolve(job, mat);
+  if (M.s_f16) mv_q4i8_body<L, CPL, GD, true>(sh, job, M, q, dq, s8q, A, ng, p0, p1, row_begin);
+  else mv_q4i8_body<L, CPL, GD, false>(sh, job, M, q, dq, s8q, A, ng, p0, p1, row_begin);
+}
+
+// Any other shape with gs a multiple of 64: one thread per (pair, output row),
+// the same sums in the same f32 order as the reference (groups in order).
+__global__ void mv_q4i8_generic_kernel(MVShape sh, MVJob job, int nmat, const int8_t* q, const float* dq,
+                                       const int* s8q) {
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  const MatRef M = resolve(job, mat);
+  const int np = p1 - p0, gx = sh.I / sh.gs;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < (long)np * sh.O; i += (long)gridDim.x * blockDim.x) {
+    const int p = p0 + (int)(i / sh.O), o = (int)(i % sh.O);
+    const uint8_t* row = M.w + (size_t)o * sh.row_bytes;
+    const int8_t* qr = q + (size_t)p * sh.I;
+    float acc = 0.f;
+    for (int g = 0; g < gx; ++g) {
+      int isum = 0;
+      for (int c = g * sh.gs; c < (g + 1) * sh.gs; c += 2) {
+        const uint32_t b = row[c >> 1] ^ (M.xor4 & 0xFFu);
+        const int k = c & 31, base = c - k;
+        isum += (int)(b & 15u) * qr[base + k / 2] + (int)(b >> 4) * qr[base + 16 + k / 2];
+      }
+      acc += (float)(isum - s8q[(size_t)p * gx + g]) *
+             (load_scale(M.s, (size_t)o * sh.G + g, M.s_f16) * dq[(size_t)p * gx + g]);
+    }
+    job.y[(size_t)p * job.ldy + o] = acc;
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 static int bytes_per_row(int fmt, int I) {
@@ -594,9 +807,14 @@ static void lanes_for(int cpr, int* L, int* A, int* cpl) {
 }
 
 // false: the shape goes to the general kernels
+// The fast kernels form row offsets with 24-bit multiplies into 32 bits.
+static bool offsets_fit(const MVShape& sh) {
+  return sh.O < (1 << 24) && (uint64_t)sh.O * (uint64_t)sh.row_bytes < (1ull << 32);
+}
+
 template <class F>
 static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
-  if (sh.cpr % 8 != 0) return false;
+  if (sh.cpr % 8 != 0 || !offsets_fit(sh)) return false;
   int L, A, cpl;
   lanes_for(sh.cpr, &L, &A, &cpl);
   const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
@@ -638,6 +856,77 @@ int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_r
   const int blocks = (int)((work + threads - 1) / threads > 4096 ? 4096 : (work + threads - 1) / threads);
   hipLaunchKernelGGL(mv_generic_kernel, dim3(blocks, nmat), dim3(threads), 0, st, sh, job, fmt, nmat);
   return check_launch("decode mat-vec (generic)");
+}
+
+int run_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int half, int gs, int8_t* q, float* d, int* s8,
+                 hipStream_t st) {
+  if (n <= 0) return MOE_OK;
+  if (gs % 64 != 0 || K % gs != 0)
+    return set_error(MOE_EUNSUPPORTED, "int8 activations: group size %d must be a multiple of 64 dividing %d", gs, K);
+  const long waves = (long)n * (K / gs);
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  switch (gs / 64) {
+    case 1: hipLaunchKernelGGL(round_q8_kernel<1>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 2: hipLaunchKernelGGL(round_q8_kernel<2>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 3: hipLaunchKernelGGL(round_q8_kernel<3>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 4: hipLaunchKernelGGL(round_q8_kernel<4>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 5: hipLaunchKernelGGL(round_q8_kernel<5>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 6: hipLaunchKernelGGL(round_q8_kernel<6>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 7: hipLaunchKernelGGL(round_q8_kernel<7>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 8: hipLaunchKernelGGL(round_q8_kernel<8>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    default: return set_error(MOE_EUNSUPPORTED, "int8 activations: group size %d (a multiple of 64 up to 512)", gs);
+  }
+  return check_launch("round activations to int8");
+}
+
+template <int L, int CPL, int GD>
+static void launch_q4i8(const MVShape& sh, const MVJob& job, int nmat, const int8_t* q, const float* dq,
+                        const int* s8q, int A, hipStream_t st) {
+  constexpr int G = CPL >= 2 ? 2 : 4;
+  constexpr int rpp = 64 / L;
+  const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));
+  int ng = (int)(groups / 2048);
+  ng = ng < 1 ? 1 : (ng > 16 ? 16 : ng);
+  const int wave_rows = ng * G * rpp;
+  const int waves = (sh.O + wave_rows - 1) / wave_rows;
+  hipLaunchKernelGGL((mv_q4i8_kernel<L, CPL, GD>), dim3((waves + 3) / 4, nmat), dim3(256), 0, st, sh, job, q, dq, s8q,
+                     A, ng);
+}
+
+template <int GD>
+static bool launch_q4i8_gd(const MVShape& sh, const MVJob& job, int nmat, const int8_t* q, const float* dq,
+                           const int* s8q, hipStream_t st) {
+  if (sh.cpr % 8 != 0 || !offsets_fit(sh)) return false;
+  int L, A, cpl;
+  lanes_for(sh.cpr, &L, &A, &cpl);
+  if (A % GD != 0) return false;
+  if (L == 64 && cpl == 1) launch_q4i8<64, 1, GD>(sh, job, nmat, q, dq, s8q, A, st);
+  else if (L == 64 && cpl == 2) launch_q4i8<64, 2, GD>(sh, job, nmat, q, dq, s8q, A, st);
+  else if (L == 64 && cpl == 4) launch_q4i8<64, 4, GD>(sh, job, nmat, q, dq, s8q, A, st);
+  else if (L == 32 && cpl == 1) launch_q4i8<32, 1, GD>(sh, job, nmat, q, dq, s8q, A, st);
+  else if (L == 16 && cpl == 1) launch_q4i8<16, 1, GD>(sh, job, nmat, q, dq, s8q, A, st);
+  else if (L == 8 && cpl == 1) launch_q4i8<8, 1, GD>(sh, job, nmat, q, dq, s8q, A, st);
+  else return false;
+  return true;
+}
+
+int run_matvec_q4i8(const MVShape& sh, const MVJob& job, int nmat, const int8_t* q, const float* dq, const int* s8q,
+                    hipStream_t st) {
+  if (nmat <= 0) return MOE_OK;
+  bool done = false;  // the rounded activations are the layer's own 256-byte aligned buffers
+  if (sh.row_bytes % 16 == 0) {
+    if (sh.gs == 64) done = launch_q4i8_gd<2>(sh, job, nmat, q, dq, s8q, st);
+    else if (sh.gs == 128) done = launch_q4i8_gd<4>(sh, job, nmat, q, dq, s8q, st);
+  }
+  if (!done) {
+    const long work = (long)job.n * sh.O;
+    long blocks = (work + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(mv_q4i8_generic_kernel, dim3((unsigned)blocks, nmat), dim3(256), 0, st, sh, job, nmat, q, dq,
+                       s8q);
+  }
+  return check_launch("int4 mat-vec, int8 activations");
 }
 
 }  // namespace moe

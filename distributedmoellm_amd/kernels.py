@@ -29,7 +29,10 @@ MAX_ROWS = 1 << 30          # every size runs on the device
 ROW_DECODE_FROM = 4         # kept for callers that split on it (moelan/kernels.py:22)
 BLAS_FROM = 8               # idem (moelan/kernels.py:23): the store sends such groups to the big-group path
 FUSED = os.environ.get("MOELAN_FUSED", "1") != "0"
-INT8_ACT = False            # the int8-activation variant of moe_q4 is not provided
+# The layer call rounds activations to int8 per group of 64 (or a multiple up to
+# 512), as moelan's int8-activation kernels do (moelan/kernels.py:28-31);
+# MOELAN_INT8_ACT=0 keeps them float (exact to the int4 weights).
+INT8_ACT = os.environ.get("MOELAN_INT8_ACT", "1") != "0"
 AVX2 = False
 
 try:
@@ -235,8 +238,9 @@ def gguf_dequant(raw, qtype: int, out):
 # ---------------------------------------------------------------- one layer
 
 def int8_act_for(H: int, I: int, gs: int) -> bool:
-    """Whether moe_q4 would round activations to int8: never here (float activations, exact)."""
-    return False
+    """Whether :func:`moe_q4` runs experts of this shape with int8 activations
+    (moelan/kernels.py:920-922; groups of up to 512 here)."""
+    return INT8_ACT and gs % 64 == 0 and gs <= 512 and H % gs == 0 and I % gs == 0
 
 
 def q4_expert_ptrs(e):
@@ -351,14 +355,36 @@ def moe_q4_run(x, meta: LayerMeta, H: int, I: int, gs: int, out, workspace=None)
     for p in meta.ptrs:
         if not all(p[:4]):
             raise ValueError("null expert address")
-    need = _lib.lib().moe_q4_layer_workspace(max(meta.P, 1), H, I)
+    i8 = int8_act_for(H, I, gs)
+    if i8:
+        name, need = "moe_q4_layer_i8", _lib.lib().moe_q4_layer_i8_workspace(max(meta.P, 1), H, I, gs)
+    else:
+        name, need = "moe_q4_layer", _lib.lib().moe_q4_layer_workspace(max(meta.P, 1), H, I)
     ws = workspace if workspace is not None and workspace.numel() >= need else \
         torch.empty(need, dtype=torch.uint8, device=xd.device)
-    _lib.call("moe_q4_layer", _ptr(xd), xd.shape[1], meta.table, None, meta.k, meta.poff, meta.prow, meta.pw,
+    _lib.call(name, _ptr(xd), xd.shape[1], meta.table, None, meta.k, meta.poff, meta.prow, meta.pw,
               meta.P, meta.rrow, meta.rptr, meta.rpair, meta.nr, _ptr(od), od.shape[1], H, I, gs,
               meta.max_rows, _ptr(ws), ws.numel(), stream_handle())
     if od is not out:
         _into(out, od)
+
+
+def round_q8(x, gs: int):
+    """Rows of ``x`` rounded to int8 per group of ``gs`` (moelan/kernels.py:
+    833-852): (q int8 (n, K), scales f32 (n, K/gs), 8 * group sums int32).
+    ``q`` keeps the columns in their own order (the device stores each 32-column
+    chunk as even columns then odd ones; this reorders it back)."""
+    _need()
+    xd = _f32(x)
+    n, K = xd.shape
+    q = torch.empty((n, K), dtype=torch.int8, device=xd.device)
+    d = torch.empty((n, K // gs), dtype=torch.float32, device=xd.device)
+    s8 = torch.empty((n, K // gs), dtype=torch.int32, device=xd.device)
+    _lib.call("moe_round_q8", _ptr(xd), K, None, n, K, int(gs), _ptr(q), _ptr(d), _ptr(s8), stream_handle())
+    q = q.view(n, K // 32, 2, 16).transpose(2, 3).reshape(n, K)
+    if is_device(x):
+        return q, d, s8
+    return q.cpu().numpy(), d.cpu().numpy(), s8.cpu().numpy()
 
 
 # ---------------------------------------------------------------- prompt reading

@@ -142,6 +142,31 @@ int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4
                           int k, const int* poff, int which, int H, int I, int gs, int max_rows, float* y, int ldy,
                           void* stream);
 
+/* ------------------------------------- the same call, int8 activations */
+
+/* Bytes of workspace moe_q4_layer_i8 needs for P pairs. */
+size_t moe_q4_layer_i8_workspace(int P, int H, int I, int gs);
+
+/* moe_q4_layer with the activations rounded to int8 per group of gs (a
+ * multiple of 64 up to 512, dividing H and I): each pair's input row, and its SiLU(gate)*up
+ * row, rounded as _round_q8; each group's product an exact integer sum of
+ * unsigned nibble * int8, added as f32(isum - 8*sum q) * (s_w * d); the same
+ * combine. The reference's int8-activation layer call: moe_q4 when
+ * int8_act_for(H, I, gs) holds, moelan/kernels.py:942-968 (_moe_q4i :854-917,
+ * _round_q8 :833-852, _q4c64 :807-831). Workspace 256-byte aligned. */
+int moe_q4_layer_i8(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k, const int* poff,
+                    const int* prow, const float* pw, int P, const int* rrow, const int* rptr, const int* rpair, int nr,
+                    float* out, int ldo, int H, int I, int gs, int max_rows, void* workspace, size_t ws_bytes,
+                    void* stream);
+
+/* Rows xrow[i] (xrow NULL: i) of x [*, ldx], i < n, rounded to int8 per group
+ * of gs (a multiple of 64 up to 512) as _round_q8, moelan/kernels.py:833-852: scale d = max|v| / 127 (1 for
+ * a zero group), q = floor(v * (1/d) + 0.5), s8 = 8 * the group's sum of q.
+ * q [n, K] bytes, each 32-column chunk as its 16 even columns then its 16 odd
+ * ones (the reference's qe / qo halves); d, s8 [n, K/gs]. All device arrays. */
+int moe_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int gs, int8_t* q, float* d, int32_t* s8,
+                 void* stream);
+
 /* ------------------------------------------------ prompt reading (prefill) */
 
 /* Bytes of workspace that let moe_router_logits split H over more workgroups. */

@@ -219,6 +219,72 @@ def moe_q4(x, items, out) -> np.ndarray:
     return res
 
 
+# ------------------------------------------------------------------ int8 activations
+
+def round_q8(v, gs: int):
+    """_round_q8 (moelan/kernels.py:833-852): a row rounded to int8 per group of gs.
+    Returns (q int32 [K] in column order, d f32 [K/gs] the group scales, s8 int32
+    [K/gs] = 8 * the sum of the group's q). f32 arithmetic as written: m = max |v|,
+    sc = m / 127 (1 when m == 0), inv = 1 / sc, q = floor(v * inv + 0.5) with the
+    product and the sum each rounded to f32."""
+    v = np.asarray(v, np.float32)
+    G = v.shape[0] // gs
+    vg = v.reshape(G, gs)
+    m = np.abs(vg).max(axis=1).astype(np.float32)
+    sc = np.where(m > 0, m / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    inv = (np.float32(1.0) / sc).astype(np.float32)
+    prod = (vg * inv[:, None]).astype(np.float32)
+    q = np.floor((prod + np.float32(0.5)).astype(np.float32)).astype(np.int32)
+    s8 = (8 * q.sum(axis=1)).astype(np.int32)
+    return q.reshape(-1), sc, s8
+
+
+def q4i8_matvec(q, d, s8, raw, s, gs: int, offset: bool) -> np.ndarray:
+    """One matrix against one int8-rounded row, as _moe_q4i's inner loop
+    (moelan/kernels.py:882-895, 898-911) with _q4c64 (:807-831): per group the
+    exact sum of unsigned nibble * q, then acc += f32(isum - s8[g]) *
+    (s[o, g] * d[g]) over the groups in order, in f32."""
+    u = q4_unpack(raw, offset).astype(np.int64)
+    O, I = u.shape
+    G = I // gs
+    isum = (u.reshape(O, G, gs) * np.asarray(q, np.int64).reshape(G, gs)[None]).sum(2)
+    sw = np.asarray(s).astype(np.float32).reshape(O, G)
+    t = (isum - np.asarray(s8, np.int64)[None, :]).astype(np.float32) * \
+        (sw * np.asarray(d, np.float32)[None, :]).astype(np.float32)
+    acc = np.zeros(O, np.float32)
+    for g in range(G):
+        acc = (acc + t[:, g].astype(np.float32)).astype(np.float32)
+    return acc
+
+
+def moe_q4i(x, items, out, H: int, I: int, gs: int) -> np.ndarray:
+    """moe_q4 with int8 activations (moelan/kernels.py:942-968 when int8_act_for
+    holds; _moe_q4i :854-917): each distinct row of x rounded to int8 per group;
+    per pair the gate|up product, SiLU(gate) * up in f32, that rounded to int8
+    per group, the down product; then part[r] += w * y[p] in pair order (f32)
+    and out[uniq] += part. items: (raw_gu, s_gu, raw_dn, s_dn, offset, rows, w)."""
+    x = np.asarray(x, np.float32)
+    rows = np.concatenate([np.asarray(it[5]) for it in items]).astype(np.int64)
+    uniq, prow = np.unique(rows, return_inverse=True)
+    rq = {int(r): round_q8(x[r], gs) for r in uniq}
+    part = np.zeros((len(uniq), H), np.float32)
+    p = 0
+    for raw_gu, s_gu, raw_dn, s_dn, offset, rws, w in items:
+        for j, r in enumerate(np.asarray(rws)):
+            q, d, s8 = rq[int(r)]
+            h = q4i8_matvec(q, d, s8, raw_gu, s_gu, gs, offset)
+            g0, up = h[:I], h[I:]
+            act = (g0 / (np.float32(1.0) + np.exp(-g0)) * up).astype(np.float32)
+            qa, da, s8a = round_q8(act, gs)
+            y = q4i8_matvec(qa, da, s8a, raw_dn, s_dn, gs, offset)
+            k = int(prow[p])
+            part[k] = (part[k] + np.float32(np.asarray(w, np.float32)[j]) * y).astype(np.float32)
+            p += 1
+    res = np.asarray(out, np.float32).copy()
+    res[uniq] = (res[uniq] + part).astype(np.float32)
+    return res
+
+
 # ------------------------------------------------------------------ routing
 
 def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:

@@ -98,3 +98,52 @@ def test_kernels_fail_loudly_without_gpu():
     with pytest.raises(RuntimeError, match="not available"):
         kernels.q4_matmul_t(np.zeros((1, 64), np.float32), np.zeros((8, 32), np.uint8),
                             np.zeros((8, 2), np.float32), 32, False)
+
+
+def test_int8_activation_calls_check_their_group_size():
+    """The int8-activation layer call and the rounding take groups of 64 or
+    multiples up to 512 (moelan/kernels.py:920-922); others are unsupported."""
+    L = _lib.lib()
+    assert L.moe_q4_layer_i8(1, 64, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 64, 64, 32, 1, 1, 1 << 20,
+                             None) == _lib.MOE_EUNSUPPORTED
+    assert "multiple of 64" in _lib.last_error()
+    assert L.moe_q4_layer_i8(1, 192, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 192, 192, 128, 128, 1, 1, 1 << 20,
+                             None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_round_q8(1, 96, None, 1, 96, 96, 1, 1, 1, None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_round_q8(1, 1024, None, 1, 1024, 1024, 1, 1, 1, None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_round_q8(1, 32, None, 1, 64, 64, 1, 1, 1, None) == _lib.MOE_EINVAL
+    assert "ldx=32" in _lib.last_error()
+    # too small a workspace is its own error, before anything runs
+    assert L.moe_q4_layer_i8(1, 128, 1, None, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1, 128, 128, 128, 64, 1, 256, 16,
+                             None) == _lib.MOE_EWORKSPACE
+    # nothing to do
+    assert L.moe_q4_layer_i8(None, 128, None, None, 0, None, None, None, 0, None, None, None, 0, None, 128,
+                             128, 128, 64, 0, None, 0, None) == 0
+    assert L.moe_round_q8(None, 128, None, 0, 128, 64, None, None, None, None) == 0
+
+
+def test_int8_activation_workspace():
+    L = _lib.lib()
+
+    def up(n):
+        return (n + 255) // 256 * 256
+    P, H, I, gs = 3, 2048, 768, 64
+    want = (up(P * 2 * I * 4) + up(P * H * 4) + up(P * H) + 2 * up(P * (H // gs) * 4) + up(P * I)
+            + 2 * up(P * (I // gs) * 4))
+    assert L.moe_q4_layer_i8_workspace(P, H, I, gs) == want
+    assert L.moe_q4_layer_i8_workspace(P, H, I, 96) == 0
+
+
+def test_int8_act_for_follows_the_reference_rule(monkeypatch):
+    """int8_act_for (moelan/kernels.py:920-922): on by default for groups of 64
+    and multiples dividing H and I; MOELAN_INT8_ACT=0 turns it off."""
+    from distributedmoellm_amd import kernels
+    monkeypatch.setattr(kernels, "INT8_ACT", True)
+    assert kernels.int8_act_for(2048, 768, 64)
+    assert kernels.int8_act_for(2048, 768, 128)
+    assert kernels.int8_act_for(1536, 384, 192)
+    assert not kernels.int8_act_for(2048, 768, 32)
+    assert not kernels.int8_act_for(2048, 800, 64)
+    assert not kernels.int8_act_for(4096, 2048, 1024)
+    monkeypatch.setattr(kernels, "INT8_ACT", False)
+    assert not kernels.int8_act_for(2048, 768, 64)

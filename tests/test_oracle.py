@@ -265,3 +265,79 @@ def test_moe_layer_matches_token_loop():
         assert idx[t].tolist() == order
         want = sum(w[t, j] * R.expert_exact(x[t:t + 1], *Ws[order[j]])[0] for j in range(k))
         np.testing.assert_allclose(out[t], want, rtol=1e-6)
+
+
+# ------------------------------------------------------------------ int8 activations
+
+def test_round_q8_rounds_half_up_and_bounds():
+    """_round_q8 (moelan/kernels.py:833-852) pinned by what it must do: a group whose
+    largest |v| is 127 has scale 1, so halves round up (floor(v + 0.5): 2.5 -> 3,
+    -2.5 -> -2, unlike numpy's round-half-even); every group's largest |v| maps to
+    127; the round trip is within half a step; a zero group has scale 1."""
+    v = np.zeros(128, np.float32)
+    v[:6] = [127.0, 2.5, -2.5, 0.5, -0.5, -127.0]
+    q, d, s8 = R.round_q8(v, 64)
+    assert d[0] == np.float32(1.0) and d[1] == np.float32(1.0)        # group 1 is all zero
+    assert q[:6].tolist() == [127, 3, -2, 1, 0, -127]
+    assert (q[64:] == 0).all() and s8[1] == 0
+    assert s8[0] == 8 * int(q[:64].sum())
+    rng = np.random.default_rng(30)
+    for gs in (64, 128):
+        x = (rng.standard_normal(512) * rng.uniform(0.01, 100, 512)).astype(np.float32)
+        q, d, s8 = R.round_q8(x, gs)
+        qg, xg = q.reshape(-1, gs), x.reshape(-1, gs).astype(np.float64)
+        assert (np.abs(qg) <= 127).all()
+        assert (np.abs(qg).max(axis=1) == 127).all()
+        err = np.abs(xg - qg * d.astype(np.float64)[:, None])
+        assert (err <= d.astype(np.float64)[:, None] * (0.5 + 1e-5)).all()
+        np.testing.assert_array_equal(s8, 8 * qg.sum(axis=1))
+
+
+def test_q4i8_matvec_one_hot_and_float64():
+    """The int8-activation product: a one-hot q (d = 1, s8 = 8) reads column k as
+    (u - 8) * s exactly; random rows agree with a float64 sum to f32 rounding."""
+    rng = np.random.default_rng(31)
+    O, I, gs = 12, 256, 64
+    raw = rng.integers(0, 256, (O, I // 2), dtype=np.uint8)
+    s = (np.abs(rng.normal(0, 0.02, (O, I // gs))) / 8).astype(np.float16)
+    W = R.q4_dequant64(raw, s, gs, False)
+    for k in (0, 1, 63, 64, 255):
+        q = np.zeros(I, np.int32)
+        q[k] = 1
+        d = np.ones(I // gs, np.float32)
+        s8 = np.zeros(I // gs, np.int32)
+        s8[k // gs] = 8
+        y = R.q4i8_matvec(q, d, s8, raw, s, gs, False)
+        np.testing.assert_array_equal(y.astype(np.float64), W[:, k])
+    x = rng.standard_normal(I).astype(np.float32)
+    q, d, s8 = R.round_q8(x, gs)
+    want = W @ (q.astype(np.float64) * np.repeat(d.astype(np.float64), gs))
+    got = R.q4i8_matvec(q, d, s8, raw, s, gs, False)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-7 * np.abs(want).max())
+
+
+def test_moe_q4i_close_to_float_layer():
+    """The int8-activation layer call against the exact float one, with the bounds
+    of the reference's own test (tests/test_fused.py:106-112): norm-wise 3e-2, per
+    row 5e-2, cosine > 0.999."""
+    rng = np.random.default_rng(32)
+    H, I, gs = 256, 128, 64
+    ex = []
+    for _ in range(4):
+        ex.append((rng.integers(0, 256, (2 * I, H // 2), dtype=np.uint8),
+                   (np.abs(rng.normal(0, 0.02, (2 * I, H // gs))) / 8).astype(np.float16),
+                   rng.integers(0, 256, (H, I // 2), dtype=np.uint8),
+                   (np.abs(rng.normal(0, 0.02, (H, I // gs))) / 8).astype(np.float16)))
+    x = rng.standard_normal((6, H)).astype(np.float32)
+    sel = [(0, [0]), (1, [0, 3]), (2, [1, 2, 3]), (3, [5])]
+    items = [(*ex[e], False, np.array(rows), rng.uniform(0.1, 1, len(rows)).astype(np.float32)) for e, rows in sel]
+    got = R.moe_q4i(x, items, np.zeros((6, H), np.float32), H, I, gs)
+    fitems = [(lambda xr, e=e: R.expert_exact(xr, R.q4_dequant64(ex[e][0], ex[e][1], gs, False),
+                                               R.q4_dequant64(ex[e][2], ex[e][3], gs, False), I), rows, w)
+              for (e, _), (_, _, _, _, _, rows, w) in zip(sel, items)]
+    want = R.moe_q4(x, fitems, np.zeros((6, H)))
+    assert np.linalg.norm(got - want) < 3e-2 * np.linalg.norm(want)
+    assert float((want * got).sum() / np.sqrt((want * want).sum() * (got * got).sum())) > 0.999
+    for r in range(6):
+        if np.abs(want[r]).max() > 0:
+            assert np.linalg.norm(got[r] - want[r]) < 5e-2 * np.linalg.norm(want[r])
