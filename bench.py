@@ -260,6 +260,49 @@ def decode384_gs64(args, L):
     return res
 
 
+GGUF_TYPES = {2: ("Q4_0", 32, 18), 3: ("Q4_1", 32, 20), 6: ("Q5_0", 32, 22), 7: ("Q5_1", 32, 24),
+              8: ("Q8_0", 32, 34), 10: ("Q2_K", 256, 84), 11: ("Q3_K", 256, 110), 12: ("Q4_K", 256, 144),
+              13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
+
+
+def gguf_matvec(args, L, target_bytes: int = 256 << 20, cols: int = 2048):
+    """Each GGUF block type's decode mat-vec (moe_gguf_matmul_t, one input row)
+    on one matrix of rows of 2048 values and about 256 MB: the kernel's
+    streaming rate against the HBM roofline. Bytes are the blocks' bytes;
+    HIP events around 20 launches on the launch stream."""
+    import torch
+    stream = torch.cuda.current_stream().cuda_stream
+    x = torch.randn((1, cols), device="cuda")
+    res = {}
+    for qt, (name, per, size) in GGUF_TYPES.items():
+        row_bytes = cols // per * size
+        O = target_bytes // row_bytes
+        raw = torch.randint(0, 256, (O, row_bytes), dtype=torch.uint8, device="cuda")
+        y = torch.empty((1, O), device="cuda")
+        for _ in range(max(2, args.warmup)):
+            rc = L.moe_gguf_matmul_t(x.data_ptr(), 1, raw.data_ptr(), qt, O, cols, y.data_ptr(), stream)
+            if rc:
+                from distributedmoellm_amd import _lib
+                raise RuntimeError(_lib.last_error())
+        n = 20
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(n):
+            L.moe_gguf_matmul_t(x.data_ptr(), 1, raw.data_ptr(), qt, O, cols, y.data_ptr(), stream)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) / n * 1e3
+        byts = O * row_bytes + cols * 4 + O * 4
+        res[name] = dict(us=round(us, 2), bytes=byts, gbs=round(byts / us / 1e3, 1),
+                         hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4))
+        log(f"gguf {name}: {O} x {cols}, {byts / 1e6:.0f} MB in {us:.1f} us = {byts / us / 1e3:.0f} GB/s")
+        del raw, y
+    torch.cuda.empty_cache()
+    res["workload"] = ("one input row against one matrix of rows of 2048 values, about 256 MB of blocks "
+                       "(every byte random, so scale fields are arbitrary f16), 20 launches")
+    return res
+
+
 def cpu_baseline_decode(seconds: float = 12.0):
     """The reference's fused layer kernel restated in C/OpenMP (oracle/cpuref.c)
     on the host cores: one token's 384 experts per call from a pool of 64
@@ -452,7 +495,7 @@ def main() -> int:
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, prefill, copy "
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, prefill, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -478,6 +521,8 @@ def main() -> int:
             res["prefill"] = prefill_c4(args, L)
         if "decode_i8" in only:
             res["decode_i8"] = decode384_gs64(args, L)
+        if "gguf" in only:
+            res["gguf"] = gguf_matvec(args, L)
         if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
             import torch
             a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -498,6 +543,7 @@ def main() -> int:
     if "per_layer_calls" in r:
         extras["per_layer_calls"] = r.pop("per_layer_calls")
     extras["decode384_gs64"] = decode384_gs64(args, L)
+    extras["gguf_matvec"] = gguf_matvec(args, L)
     if args.stack:
         extras["stack_235b"] = stack_decode(args, L)
     log("prefill (Qwen3-30B-A3B layer, T=512) ...")

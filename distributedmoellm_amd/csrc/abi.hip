@@ -6,6 +6,7 @@
 
 #include "../../include/moehip.h"
 #include "common.h"
+#include "blocks.h"
 #include "dequant.h"
 #include "layer.h"
 #include "matvec.h"
@@ -123,11 +124,18 @@ MOE_API int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* 
   return run_matvec(FMT_Q8, sh, j, 1, n, as_stream(stream));
 }
 
+// values per block of a quantized GGUF type, 0 for any other type
+static int gguf_block_values(int qtype) {
+  int per, size, vals;
+  return block_geometry(qtype, &per, &size, &vals) ? per : 0;
+}
+
+#define GGUF_TYPES "2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K"
+
 MOE_API int moe_gguf_matmul_t(const float* x, int n, const uint8_t* raw, int qtype, int O, int cols, float* y,
                               void* stream) {
-  if (qtype != FMT_Q8_0 && qtype != FMT_Q4_K)
-    return set_error(MOE_EUNSUPPORTED, "moe_gguf_matmul_t: qtype %d (supported: 8 Q8_0, 12 Q4_K)", qtype);
-  const int blk = qtype == FMT_Q8_0 ? 32 : 256;
+  const int blk = gguf_block_values(qtype);
+  if (blk == 0) return set_error(MOE_EUNSUPPORTED, "moe_gguf_matmul_t: qtype %d (supported: " GGUF_TYPES ")", qtype);
   REQUIRE(O > 0 && cols > 0 && cols % blk == 0, "moe_gguf_matmul_t: cols=%d must be a positive multiple of %d",
           cols, blk);
   REQUIRE(n >= 0, "moe_gguf_matmul_t: n=%d", n);
@@ -163,9 +171,8 @@ MOE_API int moe_q8_dequant(const int8_t* q, const void* s, int s_f16, int O, int
 }
 
 MOE_API int moe_gguf_dequant(const uint8_t* raw, int qtype, int O, int cols, float* out, void* stream) {
-  if (qtype != FMT_Q8_0 && qtype != FMT_Q4_K)
-    return set_error(MOE_EUNSUPPORTED, "moe_gguf_dequant: qtype %d (supported: 8 Q8_0, 12 Q4_K)", qtype);
-  const int blk = qtype == FMT_Q8_0 ? 32 : 256;
+  const int blk = gguf_block_values(qtype);
+  if (blk == 0) return set_error(MOE_EUNSUPPORTED, "moe_gguf_dequant: qtype %d (supported: " GGUF_TYPES ")", qtype);
   REQUIRE(O > 0 && cols > 0 && cols % blk == 0, "moe_gguf_dequant: cols=%d must be a positive multiple of %d", cols,
           blk);
   REQUIRE(raw && out, "moe_gguf_dequant: null pointer");

@@ -75,6 +75,23 @@ __device__ __forceinline__ float gguf_half(uint32_t h) {
 // g / (1 + e^-g) with the hardware exp and reciprocal (a few ulp; no IEEE divide)
 __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
+template <int CTRL, int ROWMASK, bool BC>
+__device__ __forceinline__ float dpp_read(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, BC));
+}
+
+// lane L-1 of every aligned group of L lanes (L = 8, 16, 32, 64) receives the group's sum
+template <int L>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  v += dpp_read<0x111, 0xf, true>(v);  // row_shr:1
+  v += dpp_read<0x112, 0xf, true>(v);  // row_shr:2
+  v += dpp_read<0x114, 0xf, true>(v);  // row_shr:4
+  if constexpr (L >= 16) v += dpp_read<0x118, 0xf, true>(v);   // row_shr:8
+  if constexpr (L >= 32) v += dpp_read<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1, 3
+  if constexpr (L >= 64) v += dpp_read<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // sum over aligned groups of `width` lanes (width a power of two <= 64)
 __device__ __forceinline__ float group_sum(float v, int width) {
   for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -3,12 +3,14 @@
 //   int8   q * s                moelan/kernels.py:230-237
 //   Q8_0   d * q                moelan/kernels.py:262-268
 //   Q4_K   (d*sc) * q - dmin*m  moelan/kernels.py:318-336 (no FMA contraction)
+//   the other GGUF block types: blocks.hip
 // Not on the hot path (the mat-vec and the grouped GEMM never materialise
 // f32 weights); used by the matrix objects' dequant() and by tests.
 #include "common.h"
 #include "formats.h"
 #include "dequant.h"
 #include "matvec.h"
+#include "blocks.h"
 
 namespace moe {
 
@@ -93,8 +95,10 @@ int run_dequant_q8(const int8_t* q, const void* s, int s_f16, int O, int I, int 
 int run_dequant_gguf(const uint8_t* raw, int qtype, int O, int cols, float* out, hipStream_t st) {
   if (qtype == FMT_Q8_0)
     hipLaunchKernelGGL(dq_q8_0_kernel, dim3(grid_for((long)O * cols / 32)), dim3(256), 0, st, raw, O, cols, out);
-  else
+  else if (qtype == FMT_Q4_K)
     hipLaunchKernelGGL(dq_q4_k_kernel, dim3(grid_for((long)O * cols / 64)), dim3(256), 0, st, raw, O, cols, out);
+  else
+    return run_dequant_blocks(raw, qtype, O, cols, out, st);
   return check_launch("GGUF dequant");
 }
 

@@ -9,9 +9,9 @@
 //        holds column 2j in the low and 2j+1 in the high nibble; nibbles become
 //        unsigned with XOR 0x88 (u = v + 8); one scale per gs columns.
 //   Q8   group-scaled int8 (moelan/experts.py:125-167): 16 bytes = 16 columns.
-//   Q8_0 GGUF block of 34 bytes: f16 d, then 32 int8 (moelan/kernels.py:262-268).
 //   Q4_K GGUF superblock of 144 bytes (moelan/kernels.py:310-336): a chunk is
-//        16 bytes of its nibbles (16 low + 16 high values) plus the header.
+//        16 bytes of its nibbles (16 low + 16 high values) plus the header; the
+//        GGUF mat-vec itself is in blocks.hip.
 #pragma once
 #include "common.h"
 
@@ -75,7 +75,6 @@ struct FmtQ4 {
   static constexpr int VALS = 32;   // columns per chunk
   static constexpr int XR = 33;     // activation registers per chunk and row
   static constexpr int BYTES = 16;
-  static constexpr bool GGUF = false;
 
   // xr[m] = x[2m] - x[2m+1]/16, xr[16+m] = x[2m+1]/16, xr[32] = sum of the 32.
   // With u-nibbles lo, hi and the byte b = lo + 16 hi of byte m:
@@ -117,7 +116,6 @@ struct FmtQ8 {
   static constexpr int VALS = 16;
   static constexpr int XR = 16;
   static constexpr int BYTES = 16;
-  static constexpr bool GGUF = false;
 
   __device__ static void load_x(const XSrc& xs, int chunk, float* xr) { xs.run<16>(chunk * 16, xr); }
 
@@ -132,54 +130,9 @@ struct FmtQ8 {
   }
 };
 
-// ------------------------------------------------------------------ GGUF Q8_0
-struct FmtQ8_0 {
-  static constexpr int VALS = 32;
-  static constexpr int XR = 32;
-  static constexpr int BYTES = 34;
-  static constexpr bool GGUF = true;
-
-  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) { xs.run<32>(chunk * 32, xr); }
-
-  // One block at byte offset 34*chunk. With a 4-byte aligned row start only
-  // aligned dword (and one ushort) loads are used, realigned with v_alignbyte;
-  // otherwise bytes.
-  __device__ static float block_dot(const uint8_t* row, int chunk, const float* xr, bool a4) {
-    const int off = chunk * 34;
-    float acc = 0.f;
-    if (!a4) {
-      const uint8_t* b = row + off;
-#pragma unroll
-      for (int j = 0; j < 32; ++j) acc = fmaf((float)(int8_t)b[2 + j], xr[j], acc);
-      return gguf_half(b[0] | (b[1] << 8)) * acc;
-    }
-    const int sh = off & 3;  // 0 or 2
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (off - sh));
-    uint32_t d[9];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) d[j] = __builtin_nontemporal_load(p + j);
-    // bytes 32..35 of the window: all four are the block's when sh == 2; when
-    // sh == 0 only two are, so read just those
-    if (sh) d[8] = __builtin_nontemporal_load(p + 8);
-    else d[8] = *reinterpret_cast<const uint16_t*>(row + off + 32);
-    const float scale = gguf_half(sh ? (d[0] >> 16) : (d[0] & 0xFFFFu));
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t q = sh ? d[j + 1] : __builtin_amdgcn_alignbyte(d[j + 1], d[j], 2);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) acc = fmaf((float)(int8_t)(q >> (8 * k)), xr[4 * j + k], acc);
-    }
-    return scale * acc;
-  }
-};
-
 // ------------------------------------------------------------------ GGUF Q4_K
+// Q4_K helpers shared by the block mat-vec (blocks.hip) and the dequant
 struct FmtQ4K {
-  static constexpr int VALS = 32;
-  static constexpr int XR = 34;
-  static constexpr int BYTES = 16;
-  static constexpr bool GGUF = true;
-
   // chunk c: superblock c/8, nibble group kk = (c%8)/2, half = c%2. Its 16
   // bytes give values 64kk + 16half + l (low nibble, sub-block 2kk) and
   // 64kk + 32 + 16half + l (high nibble, sub-block 2kk+1), l = 0..15.
@@ -228,30 +181,6 @@ struct FmtQ4K {
     const uint8_t* p;
     __device__ int operator()(int i) const { return p[i]; }
   };
-
-  // d*(sc1*sum lo*x + sc2*sum hi*x) - dmin*(m1*sum x_lo + m2*sum x_hi)
-  // (moelan/kernels.py:499-527, one lane's half of a 32-value sub-block pair)
-  __device__ static float dot(const uint4 hdr, const uint4 q, int chunk, const float* xr) {
-    const int kk = (chunk & 7) >> 1;
-    const float d = gguf_half(hdr.x & 0xFFFFu), dmin = gguf_half(hdr.x >> 16);
-    const HdrBytes sb{hdr.y, hdr.z, hdr.w};
-    int sc1, m1, sc2, m2;
-    scale_min(2 * kk, sb, sc1, m1);
-    scale_min(2 * kk + 1, sb, sc2, m2);
-    const uint32_t a[4] = {q.x, q.y, q.z, q.w};
-    float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = opaque(a[i] & 0x0F0F0F0Fu);
-      const uint32_t hi = opaque((a[i] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        s1 = fmaf(ubyte(lo, k), xr[4 * i + k], s1);
-        s2 = fmaf(ubyte(hi, k), xr[16 + 4 * i + k], s2);
-      }
-    }
-    return d * ((float)sc1 * s1 + (float)sc2 * s2) - dmin * ((float)m1 * xr[32] + (float)m2 * xr[33]);
-  }
 };
 
 }  // namespace moe

@@ -5,7 +5,21 @@
 
 namespace moe {
 
-enum { FMT_Q4 = 0, FMT_Q8 = 1, FMT_Q8_0 = 8, FMT_Q4_K = 12 };  // GGUF ids as ggml's
+// GGUF ids as ggml's; FMT_Q4 and FMT_Q8 are colibri's int4 and int8
+enum {
+  FMT_Q4 = 0,
+  FMT_Q8 = 1,
+  FMT_Q4_0 = 2,
+  FMT_Q4_1 = 3,
+  FMT_Q5_0 = 6,
+  FMT_Q5_1 = 7,
+  FMT_Q8_0 = 8,
+  FMT_Q2_K = 10,
+  FMT_Q3_K = 11,
+  FMT_Q4_K = 12,
+  FMT_Q5_K = 13,
+  FMT_Q6_K = 14
+};
 
 // One int4 expert as the fused layer call reads it; the layout of
 // moe_q4_expert in include/moehip.h.
@@ -47,6 +61,18 @@ struct MVJob {
   int which;    // 0: gate|up of the descriptor, 1: down
   int half_in;  // > 0: input rows are h = gate|up (2*half_in wide), use silu(gate)*up
 };
+
+// the matrix a launch's blockIdx.y reads
+__device__ __forceinline__ MatRef resolve(const MVJob& job, int mat) {
+  if (job.experts == nullptr) return job.single;
+  const ExpertDesc& e = job.experts[job.eidx ? job.eidx[mat] : mat];
+  MatRef m;
+  m.w = job.which ? e.dn_w : e.gu_w;
+  m.s = job.which ? e.dn_s : e.gu_s;
+  m.xor4 = e.xor8 * 0x01010101u;
+  m.s_f16 = e.s_f16;
+  return m;
+}
 
 int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh);
 // rows xrow[p] (or p) of x, or silu(h[:, :half]) * h[:, half:] when half > 0,

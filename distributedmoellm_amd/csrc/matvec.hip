@@ -18,6 +18,7 @@
 #include "common.h"
 #include "formats.h"
 #include "matvec.h"
+#include "blocks.h"
 
 #include <stdlib.h>
 
@@ -36,16 +37,6 @@ __device__ __forceinline__ uint4 load16(const uint8_t* p, bool a16) {
   return uint4{v[0], v[1], v[2], v[3]};
 }
 
-__device__ __forceinline__ MatRef resolve(const MVJob& job, int mat) {
-  if (job.experts == nullptr) return job.single;
-  const ExpertDesc& e = job.experts[job.eidx ? job.eidx[mat] : mat];
-  MatRef m;
-  m.w = job.which ? e.dn_w : e.gu_w;
-  m.s = job.which ? e.dn_s : e.gu_s;
-  m.xor4 = e.xor8 * 0x01010101u;
-  m.s_f16 = e.s_f16;
-  return m;
-}
 
 // Adds the partials of a pass and writes y; `acc` is [PASSES][NR].
 template <int PASSES, int NR>
@@ -134,76 +125,6 @@ __global__ __launch_bounds__(256) void mv_kernel(MVShape sh, MVJob job) {
   }
 }
 
-// GGUF: the block scale lives in the weight bytes, so the chunk is handled by
-// the format's own routine.
-template <class F, int NR, int PASSES>
-__global__ __launch_bounds__(256) void mv_gguf_kernel(MVShape sh, MVJob job) {
-  extern __shared__ float red[];
-  const int mat = blockIdx.y;
-  int p0 = 0, p1 = job.n;
-  if (job.seg) {
-    p0 = job.seg[mat];
-    p1 = job.seg[mat + 1];
-  }
-  if (p0 >= p1) return;
-  const MatRef M = resolve(job, mat);
-  const int t = threadIdx.x;
-  const int c = t % sh.cpr, rs = t / sh.cpr;
-  const bool lane_on = rs < sh.rpp;
-  const int row0 = blockIdx.x * sh.rpp * PASSES;
-  const bool a16 = aligned(M.w, 16), a4 = aligned(M.w, 4) && sh.row_bytes % 4 == 0;
-
-  for (int pb = p0; pb < p1; pb += NR) {
-    float xr[NR][F::XR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      if (lane_on && pb + r < p1) {
-        const int p = pb + r;
-        const int xrow = job.xrow ? job.xrow[p] : p;
-        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
-        F::load_x(xs, c, xr[r]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < F::XR; ++j) xr[r][j] = 0.f;
-      }
-    }
-    float acc[PASSES][NR];
-    if constexpr (F::BYTES == 34) {
-#pragma unroll
-      for (int k = 0; k < PASSES; ++k) {
-        const int o = row0 + k * sh.rpp + rs;
-        const bool on = lane_on && o < sh.O;
-#pragma unroll
-        for (int r = 0; r < NR; ++r)
-          acc[k][r] = on ? F::block_dot(M.w + (size_t)o * sh.row_bytes, c, xr[r], a4) : 0.f;
-      }
-    } else {
-      uint4 hdr[PASSES], q[PASSES];
-      const int sb = c >> 3;
-#pragma unroll
-      for (int k = 0; k < PASSES; ++k) {
-        const int o = row0 + k * sh.rpp + rs;
-        if (lane_on && o < sh.O) {
-          const uint8_t* blk = M.w + (size_t)o * sh.row_bytes + (size_t)sb * 144;
-          hdr[k] = load16(blk, a16);
-          q[k] = load16(blk + 16 + 16 * (c & 7), a16);
-        } else {
-          hdr[k] = uint4{};
-          q[k] = uint4{};
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < PASSES; ++k) {
-        const int o = row0 + k * sh.rpp + rs;
-        const bool on = lane_on && o < sh.O;
-#pragma unroll
-        for (int r = 0; r < NR; ++r) acc[k][r] = on ? F::dot(hdr[k], q[k], c, xr[r]) : 0.f;
-      }
-    }
-    reduce_store<PASSES, NR>(sh, job, acc, row0, rs, c, pb, p1, red);
-  }
-}
-
 // ------------------------------------------------------------------ streaming kernel
 //
 // The decode kernel for rows whose chunk count is a multiple of 8 (every
@@ -214,23 +135,6 @@ __global__ __launch_bounds__(256) void mv_gguf_kernel(MVShape sh, MVJob job) {
 // and a row's partial sums are added across its L lanes with DPP row shifts /
 // broadcasts (v_add_f32_dpp: no LDS, no barrier). Waves of a block are
 // independent.
-
-template <int CTRL, int ROWMASK, bool BC>
-__device__ __forceinline__ float dpp_read(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, BC));
-}
-
-// lane L-1 of every aligned group of L lanes receives the group's sum
-template <int L>
-__device__ __forceinline__ float lane_group_sum(float v) {
-  v += dpp_read<0x111, 0xf, true>(v);  // row_shr:1
-  v += dpp_read<0x112, 0xf, true>(v);  // row_shr:2
-  v += dpp_read<0x114, 0xf, true>(v);  // row_shr:4
-  if constexpr (L >= 16) v += dpp_read<0x118, 0xf, true>(v);   // row_shr:8
-  if constexpr (L >= 32) v += dpp_read<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1, 3
-  if constexpr (L >= 64) v += dpp_read<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2, 3
-  return v;
-}
 
 // passes per register buffer, by chunks per lane and input rows
 template <int CPL, int NR>
@@ -404,8 +308,9 @@ __global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int
   }
 }
 
-// Any shape the chunked kernels do not take (group sizes that split a chunk,
-// unaligned rows): one thread per (output row, input row), straight loops.
+// Any int4 / int8 shape the chunked kernels do not take (group sizes that split
+// a chunk, unaligned rows): one thread per (output row, input row), straight
+// loops. (GGUF rows of any alignment go to blocks.hip.)
 __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
   const int mat = blockIdx.y;
   int p0 = 0, p1 = job.n;
@@ -432,7 +337,7 @@ __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
         }
         acc = fmaf(part, load_scale(M.s, (size_t)o * sh.G + g, M.s_f16), acc);
       }
-    } else if (fmt == FMT_Q8) {
+    } else {  // Q8
       for (int g = 0; g < sh.G; ++g) {
         float part = 0.f;
         for (int j = 0; j < sh.gs; ++j) {
@@ -440,35 +345,6 @@ __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
           part = fmaf((float)(int8_t)row[col], xs(col), part);
         }
         acc = fmaf(part, load_scale(M.s, (size_t)o * sh.G + g, M.s_f16), acc);
-      }
-    } else if (fmt == FMT_Q8_0) {
-      for (int b = 0; b < sh.I / 32; ++b) {
-        const uint8_t* blk = row + 34 * b;
-        const float d = gguf_half(blk[0] | (blk[1] << 8));
-        float s = 0.f;
-        for (int j = 0; j < 32; ++j) s = fmaf((float)(int8_t)blk[2 + j], xs(b * 32 + j), s);
-        acc = fmaf(d, s, acc);
-      }
-    } else {  // Q4_K
-      for (int b = 0; b < sh.I / 256; ++b) {
-        const uint8_t* blk = row + 144 * b;
-        const float d = gguf_half(blk[0] | (blk[1] << 8)), dmin = gguf_half(blk[2] | (blk[3] << 8));
-        for (int kk = 0; kk < 4; ++kk) {
-          int sc1, m1, sc2, m2;
-          const FmtQ4K::MemBytes sb{blk + 4};
-          FmtQ4K::scale_min(2 * kk, sb, sc1, m1);
-          FmtQ4K::scale_min(2 * kk + 1, sb, sc2, m2);
-          float s1 = 0.f, s2 = 0.f, x1 = 0.f, x2 = 0.f;
-          for (int l = 0; l < 32; ++l) {
-            const uint32_t v = blk[16 + 32 * kk + l];
-            const float xa = xs(b * 256 + kk * 64 + l), xb = xs(b * 256 + kk * 64 + 32 + l);
-            s1 = fmaf((float)(v & 15u), xa, s1);
-            s2 = fmaf((float)(v >> 4), xb, s2);
-            x1 += xa;
-            x2 += xb;
-          }
-          acc += d * ((float)sc1 * s1 + (float)sc2 * s2) - dmin * ((float)m1 * x1 + (float)m2 * x2);
-        }
       }
     }
     job.y[(size_t)p * job.ldy + o] = acc;
@@ -694,20 +570,18 @@ static int bytes_per_row(int fmt, int I) {
   switch (fmt) {
     case FMT_Q4: return I / 2;
     case FMT_Q8: return I;
-    case FMT_Q8_0: return I / 32 * 34;
-    case FMT_Q4_K: return I / 256 * 144;
   }
-  return 0;
+  int per, size, vals;
+  return block_geometry(fmt, &per, &size, &vals) ? I / per * size : 0;
 }
 
 static int vals_per_chunk(int fmt) {
   switch (fmt) {
     case FMT_Q4: return 32;
     case FMT_Q8: return 16;
-    case FMT_Q8_0: return 32;
-    case FMT_Q4_K: return 32;
   }
-  return 0;
+  int per, size, vals;
+  return block_geometry(fmt, &per, &size, &vals) ? vals : 0;
 }
 
 int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh) {
@@ -730,8 +604,6 @@ static bool chunked_ok(int fmt, const MVShape& sh) {
   switch (fmt) {
     case FMT_Q4: return sh.I % 32 == 0 && sh.gs % 32 == 0 && sh.row_bytes % 16 == 0;
     case FMT_Q8: return sh.I % 16 == 0 && sh.gs % 16 == 0 && sh.row_bytes % 16 == 0;
-    case FMT_Q8_0: return sh.I % 32 == 0;
-    case FMT_Q4_K: return sh.I % 256 == 0;
   }
   return false;
 }
@@ -742,8 +614,7 @@ static void launch_nr(const MVShape& sh, const MVJob& job, int nmat, hipStream_t
   dim3 grid((sh.O + rows_per_block - 1) / rows_per_block, nmat);
   dim3 block(sh.rpp * sh.cpr);
   const size_t lds = sh.pow2 ? 0 : (size_t)PASSES * NR * sh.rpp * (sh.cpr + 1) * sizeof(float);
-  if constexpr (F::GGUF) hipLaunchKernelGGL((mv_gguf_kernel<F, NR, PASSES>), grid, block, lds, st, sh, job);
-  else hipLaunchKernelGGL((mv_kernel<F, NR, PASSES>), grid, block, lds, st, sh, job);
+  hipLaunchKernelGGL((mv_kernel<F, NR, PASSES>), grid, block, lds, st, sh, job);
 }
 
 template <class F>
@@ -836,6 +707,8 @@ static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_r
 
 int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   if (max_rows <= 0 || nmat <= 0 || sh.O <= 0) return MOE_OK;
+  int per, size, vals;
+  if (block_geometry(fmt, &per, &size, &vals)) return run_matvec_blocks(fmt, sh, job, nmat, st);  // GGUF
   if (chunked_ok(fmt, sh)) {
     if (fmt == FMT_Q4 && launch_fast<FmtQ4>(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec");
     if (fmt == FMT_Q8 && launch_fast<FmtQ8>(sh, job, nmat, max_rows, st)) return check_launch("int8 mat-vec");
@@ -845,8 +718,6 @@ int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_r
       switch (fmt) {
         case FMT_Q4: launch_fmt<FmtQ4>(sh, job, nmat, max_rows, st); break;
         case FMT_Q8: launch_fmt<FmtQ8>(sh, job, nmat, max_rows, st); break;
-        case FMT_Q8_0: launch_fmt<FmtQ8_0>(sh, job, nmat, max_rows, st); break;
-        case FMT_Q4_K: launch_fmt<FmtQ4K>(sh, job, nmat, max_rows, st); break;
       }
       return check_launch("decode mat-vec");
     }

@@ -149,7 +149,9 @@ class Expert:
                 n, H = xd.shape
                 out = torch.zeros((n, H), dtype=torch.float32, device=xd.device)
                 rows = np.arange(n, dtype=np.int32)
-                kernels.moe_q4(xd, [(ptrs, rows, np.ones(n, np.float32))], H, self.inter, self.gu.gs, out)
+                # float activations, as the reference's per-matrix expert call
+                kernels.moe_q4(xd, [(ptrs, rows, np.ones(n, np.float32))], H, self.inter, self.gu.gs, out,
+                               int8=False)
                 return out if kernels.is_device(x) else out.cpu().numpy()
         h = self.gu.matmul_t(kernels.to_device(x, torch.float32))
         a = silu_mul(h, self.inter)

@@ -3,8 +3,9 @@
 Mirrors ``moelan/gguf.py``'s quantized-matrix part: ``QTYPES`` (36-42),
 ``dequantize`` (258-275), ``QuantMatrix`` (278-314), ``Stacked`` (317-333),
 ``random_blocks`` (547-555) and ``synthetic_expert`` (558-564). The rows keep
-their GGUF bytes (one device copy, uploaded on first use); Q8_0 and Q4_K run on
-the HIP kernels, other types are not provided.
+their GGUF bytes (one device copy, uploaded on first use); every quantized
+type (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K) runs on the
+HIP kernels. F32 / F16 / BF16 tensors are not expert weights here.
 """
 
 from __future__ import annotations
@@ -20,7 +21,11 @@ QTYPES = {0: ("F32", 1, 4), 1: ("F16", 1, 2), 2: ("Q4_0", 32, 18), 3: ("Q4_1", 3
           14: ("Q6_K", 256, 210), 30: ("BF16", 1, 2)}
 QTYPE_IDS = {v[0]: k for k, v in QTYPES.items()}
 QUANTIZED = {k for k, v in QTYPES.items() if v[1] > 1}
-SUPPORTED = {8, 12}   # the types these kernels run
+SUPPORTED = QUANTIZED   # the types these kernels run
+
+# offsets of the f16 scale fields in each block (moelan/gguf.py:543-545)
+_SCALE_FIELDS = {2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 8: (0,), 10: (80, 82), 11: (108,),
+                 12: (0, 2), 13: (0, 2), 14: (208,)}
 
 
 def dequantize(raw, qtype: int, cols: int, out=None):
@@ -98,7 +103,7 @@ def random_blocks(rows: int, cols: int, qtype: int, rng=None, scale: float | Non
     rng = rng or np.random.default_rng(0)
     _, block, size = QTYPES[qtype]
     raw = rng.integers(0, 256, (rows, cols // block, size), dtype=np.uint8)
-    fields = {8: (0,), 12: (0, 2)}.get(qtype, ())
+    fields = _SCALE_FIELDS.get(qtype, ())
     for off in fields:
         if scale is None:
             v = np.abs(rng.normal(0.0, 0.01, (rows, cols // block))).astype(np.float16)

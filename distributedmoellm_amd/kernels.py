@@ -171,11 +171,15 @@ def gguf_matmul_t(x, raw, qtype: int, cols: int):
     return _ret(y, x)
 
 
+# quantized GGUF type id -> (values, bytes) per block (moelan/gguf.py:36-42)
+_GGUF_BLOCKS = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 10: (256, 84),
+                11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
 def _check_gguf(rd, qtype: int, cols: int) -> None:
-    blocks = {8: (32, 34), 12: (256, 144)}
-    if qtype not in blocks:
-        raise ValueError(f"GGUF type {qtype} is not supported (8 Q8_0, 12 Q4_K)")
-    per, size = blocks[qtype]
+    if qtype not in _GGUF_BLOCKS:
+        raise ValueError(f"GGUF type {qtype} is not a quantized type ({sorted(_GGUF_BLOCKS)})")
+    per, size = _GGUF_BLOCKS[qtype]
     if cols % per or rd.numel() != rd.shape[0] * (cols // per) * size:
         raise ValueError(f"GGUF rows of {rd.numel() // max(rd.shape[0], 1)} bytes do not hold {cols} type-{qtype} values")
 
@@ -331,19 +335,20 @@ class LayerMeta:
             raise ValueError("negative row index")
 
 
-def moe_q4(x, items, H: int, I: int, gs: int, out) -> None:
+def moe_q4(x, items, H: int, I: int, gs: int, out, int8: bool | None = None) -> None:
     """Add ``sum_e w * expert_e(x[rows])`` into ``out`` for int4 experts in one
     call (moelan/kernels.py:942-968). ``items``: (ptrs from
     :func:`q4_expert_ptrs`, rows, gate weights) per expert; the experts'
-    device arrays must stay alive until the call has run."""
+    device arrays must stay alive until the call has run. Activations are
+    rounded to int8 when :func:`int8_act_for` says so (``int8`` overrides)."""
     _need()
     if not items:
         return
     meta = LayerMeta([p for p, _, _ in items], [r for _, r, _ in items], [w for _, _, w in items])
-    moe_q4_run(x, meta, H, I, gs, out)
+    moe_q4_run(x, meta, H, I, gs, out, int8=int8)
 
 
-def moe_q4_run(x, meta: LayerMeta, H: int, I: int, gs: int, out, workspace=None) -> None:
+def moe_q4_run(x, meta: LayerMeta, H: int, I: int, gs: int, out, workspace=None, int8: bool | None = None) -> None:
     """The layer call on pair lists already on the device."""
     _need()
     xd = _f32(x)
@@ -355,8 +360,11 @@ def moe_q4_run(x, meta: LayerMeta, H: int, I: int, gs: int, out, workspace=None)
     for p in meta.ptrs:
         if not all(p[:4]):
             raise ValueError("null expert address")
-    i8 = int8_act_for(H, I, gs)
-    if i8:
+    if int8 is None:
+        int8 = int8_act_for(H, I, gs)
+    elif int8 and not (gs % 64 == 0 and gs <= 512 and H % gs == 0 and I % gs == 0):
+        raise ValueError(f"int8 activations need groups of 64 (or a multiple up to 512) dividing H and I, not {gs}")
+    if int8:
         name, need = "moe_q4_layer_i8", _lib.lib().moe_q4_layer_i8_workspace(max(meta.P, 1), H, I, gs)
     else:
         name, need = "moe_q4_layer", _lib.lib().moe_q4_layer_workspace(max(meta.P, 1), H, I)

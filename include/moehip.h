@@ -15,8 +15,9 @@
  *                   Scales [O, I/gs], f32 or f16 (s_f16 != 0).
  *                   moelan/experts.py:170-236, moelan/tiny.py:94-106
  *   int8 "GroupQuant" q int8 [O, I], scales [O, I/gs]. moelan/experts.py:125-167
- *   GGUF            raw uint8 [O, row bytes], qtype 8 (Q8_0) or 12 (Q4_K).
- *                   moelan/gguf.py:36-42, moelan/kernels.py:262-336
+ *   GGUF            raw uint8 [O, row bytes], a quantized ggml type: 2 Q4_0,
+ *                   3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K,
+ *                   13 Q5_K, 14 Q6_K. moelan/gguf.py:36-42, moelan/kernels.py:262-476
  */
 #ifndef MOEHIP_H
 #define MOEHIP_H
@@ -68,9 +69,11 @@ int moe_q4_matmul_t(const float* x, int n, const uint8_t* raw, const void* s, in
 int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* s, int s_f16, int O, int I, int gs,
                     float* y, void* stream);
 
-/* y[n, O] = x[n, cols] @ W.T for GGUF block-quantized rows (qtype 8 or 12).
+/* y[n, O] = x[n, cols] @ W.T for GGUF block-quantized rows of any quantized
+ * type, cols <= 8192; rows need no alignment.
  * Replaces gguf_matmul_t(x, raw, qtype, cols), moelan/kernels.py:981-998
- * (_mv_q8_0 :482-497, _mv_q4_k :499-527, _gguf_mm :678-691). */
+ * (_mv_q8_0 :482-498, _mv_q4_k :499-528, _mv_q5_k :529-561, _mv_q6_k
+ * :562-596, _mv_q2_k :597-632, _mv_q3_k :642-677, _gguf_mm :678-691). */
 int moe_gguf_matmul_t(const float* x, int n, const uint8_t* raw, int qtype, int O, int cols, float* y,
                       void* stream);
 

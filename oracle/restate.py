@@ -23,7 +23,7 @@ QTYPES = {0: ("F32", 1, 4), 1: ("F16", 1, 2), 2: ("Q4_0", 32, 18), 3: ("Q4_1", 3
           6: ("Q5_0", 32, 22), 7: ("Q5_1", 32, 24), 8: ("Q8_0", 32, 34), 10: ("Q2_K", 256, 84),
           11: ("Q3_K", 256, 110), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176),
           14: ("Q6_K", 256, 210), 30: ("BF16", 1, 2)}
-Q8_0, Q4_K = 8, 12
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 2, 3, 6, 7, 8, 10, 11, 12, 13, 14
 
 
 # ------------------------------------------------------------------ int4 / int8
@@ -155,13 +155,164 @@ def dq_q4_k(raw: np.ndarray, cols: int) -> np.ndarray:
     return out.reshape(rows, cols)
 
 
+def _blocks(raw: np.ndarray, cols: int, qtype: int) -> np.ndarray:
+    _, per, size = QTYPES[qtype]
+    return np.asarray(raw).reshape(raw.shape[0], cols // per, size)
+
+
+def _f32(v) -> np.ndarray:
+    return np.asarray(v).astype(np.float32)
+
+
+def dq_q4_0(raw: np.ndarray, cols: int) -> np.ndarray:
+    """18-byte blocks (moelan/kernels.py:270-278): f16 d, 16 bytes; byte j holds
+    value j (low nibble) and j+16 (high); w = d * (q - 8)."""
+    b = _blocks(raw, cols, Q4_0)
+    d = gguf_f16(b[..., 0], b[..., 1])[..., None]
+    q = b[..., 2:18].astype(np.int32)
+    return np.concatenate([d * _f32((q & 15) - 8), d * _f32((q >> 4) - 8)], -1).reshape(raw.shape[0], cols)
+
+
+def dq_q4_1(raw: np.ndarray, cols: int) -> np.ndarray:
+    """20-byte blocks (moelan/kernels.py:280-289): f16 d, f16 min, 16 bytes; w = d * q + min."""
+    b = _blocks(raw, cols, Q4_1)
+    d = gguf_f16(b[..., 0], b[..., 1])[..., None]
+    mn = gguf_f16(b[..., 2], b[..., 3])[..., None]
+    q = b[..., 4:20].astype(np.int32)
+    return np.concatenate([d * _f32(q & 15) + mn, d * _f32(q >> 4) + mn], -1).reshape(raw.shape[0], cols)
+
+
+def dq_q5(raw: np.ndarray, cols: int, with_min: bool) -> np.ndarray:
+    """Q5_0 (22 bytes: d, 32-bit qh, 16 bytes) and Q5_1 (24 bytes: d, min, qh, 16
+    bytes), moelan/kernels.py:291-308: value j (< 16) is the low nibble of byte j
+    with qh bit j as bit 4, value j+16 the high nibble with qh bit j+16; Q5_0
+    subtracts 16. w = d * q + min (min 0.0 for Q5_0, so -0.0 becomes +0.0)."""
+    qt = Q5_1 if with_min else Q5_0
+    b = _blocks(raw, cols, qt)
+    d = gguf_f16(b[..., 0], b[..., 1])[..., None]
+    mn = gguf_f16(b[..., 2], b[..., 3])[..., None] if with_min else np.float32(0.0)
+    h0 = 4 if with_min else 2
+    qh = (b[..., h0].astype(np.int64) | (b[..., h0 + 1].astype(np.int64) << 8)
+          | (b[..., h0 + 2].astype(np.int64) << 16) | (b[..., h0 + 3].astype(np.int64) << 24))[..., None]
+    q = b[..., h0 + 4:h0 + 20].astype(np.int64)
+    j = np.arange(16)
+    off = 0 if with_min else 16
+    x0 = ((q & 15) | (((qh >> j) << 4) & 0x10)) - off
+    x1 = ((q >> 4) | ((qh >> (j + 12)) & 0x10)) - off
+    return np.concatenate([d * _f32(x0) + mn, d * _f32(x1) + mn], -1).astype(np.float32).reshape(raw.shape[0], cols)
+
+
+def dq_q2_k(raw: np.ndarray, cols: int) -> np.ndarray:
+    """84-byte superblocks (moelan/kernels.py:389-415): 16 scale bytes (low
+    nibble scale, high nibble min, one per 16 values), 64 bytes of 2-bit values,
+    f16 d at 80, dmin at 82. Value n*128 + 32j + 16s + l is bits 2j of byte
+    16 + 32n + 16s + l, with scale byte 8n + 2j + s; w = (d*sc)*q - dmin*m."""
+    b = _blocks(raw, cols, Q2_K)
+    rows, nb = b.shape[:2]
+    d = gguf_f16(b[..., 80], b[..., 81])
+    dmin = gguf_f16(b[..., 82], b[..., 83])
+    out = np.empty((rows, nb, 2, 4, 2, 16), np.float32)
+    for n in range(2):
+        for j in range(4):
+            for s_ in range(2):
+                sc = b[..., 8 * n + 2 * j + s_].astype(np.int32)
+                dl, ml = d * _f32(sc & 15), dmin * _f32(sc >> 4)
+                q = (b[..., 16 + 32 * n + 16 * s_:16 + 32 * n + 16 * s_ + 16].astype(np.int32) >> (2 * j)) & 3
+                out[:, :, n, j, s_] = dl[..., None] * _f32(q) - ml[..., None]
+    return out.reshape(rows, cols)
+
+
+def q3_k_scales(sb: np.ndarray) -> np.ndarray:
+    """The 16 six-bit scales (minus 32) of Q3_K from its 12 bytes (moelan/kernels.py:
+    418-431; the same rule as _q3_scale :634-641): scale i takes byte (i & 7)'s low
+    (i < 8) or high nibble and bits 2*(i // 4) of byte 8 + i % 4 above them."""
+    s = sb.astype(np.int32)
+    out = np.empty(s.shape[:-1] + (16,), np.int32)
+    for i in range(16):
+        lo = s[..., i & 7]
+        lo = (lo & 15) if i < 8 else (lo >> 4)
+        out[..., i] = (lo | (((s[..., 8 + i % 4] >> (2 * (i // 4))) & 3) << 4)) - 32
+    return out
+
+
+def dq_q3_k(raw: np.ndarray, cols: int) -> np.ndarray:
+    """110-byte superblocks (moelan/kernels.py:416-454): 32 hmask bytes, 64 bytes of
+    2-bit values, 12 scale bytes, f16 d at 108. Value y = n*128 + 32j + 16s + l:
+    bits 2j of byte 32 + 32n + 16s + l, minus 4 unless bit (4n + j) of hmask byte
+    16s + l is set; scale 8n + 2j + s; w = (d*sc) * v."""
+    b = _blocks(raw, cols, Q3_K)
+    rows, nb = b.shape[:2]
+    d = gguf_f16(b[..., 108], b[..., 109])
+    scales = q3_k_scales(b[..., 96:108])
+    out = np.empty((rows, nb, 2, 4, 2, 16), np.float32)
+    for n in range(2):
+        for j in range(4):
+            for s_ in range(2):
+                dl = d * _f32(scales[..., 8 * n + 2 * j + s_])
+                q = (b[..., 32 + 32 * n + 16 * s_:48 + 32 * n + 16 * s_].astype(np.int32) >> (2 * j)) & 3
+                h = (b[..., 16 * s_:16 * s_ + 16].astype(np.int32) >> (4 * n + j)) & 1
+                out[:, :, n, j, s_] = dl[..., None] * _f32(q - np.where(h != 0, 0, 4))
+    return out.reshape(rows, cols)
+
+
+def dq_q5_k(raw: np.ndarray, cols: int) -> np.ndarray:
+    """176-byte superblocks (moelan/kernels.py:338-362): d, dmin, 12 scale bytes
+    (as Q4_K), 32 qh bytes at 16, 128 nibble bytes at 48. For k = 0..3, byte
+    48 + 32k + l gives value 64k + l (low nibble, qh bit 2k) and 64k + 32 + l
+    (high nibble, qh bit 2k+1) of qh byte l; w = (d*sc) * (q + 16h) - dmin*m."""
+    b = _blocks(raw, cols, Q5_K)
+    rows, nb = b.shape[:2]
+    d = gguf_f16(b[..., 0], b[..., 1])
+    dmin = gguf_f16(b[..., 2], b[..., 3])
+    sc = b[..., 4:16]
+    qh = b[..., 16:48].astype(np.int32)
+    qs = b[..., 48:].reshape(rows, nb, 4, 32).astype(np.int32)
+    out = np.empty((rows, nb, 4, 64), np.float32)
+    for k in range(4):
+        s1, m1 = scale_min_k4(2 * k, sc)
+        s2, m2 = scale_min_k4(2 * k + 1, sc)
+        d1, mm1 = d * _f32(s1), dmin * _f32(m1)
+        d2, mm2 = d * _f32(s2), dmin * _f32(m2)
+        lo = (qs[:, :, k] & 15) + np.where(qh & (1 << (2 * k)), 16, 0)
+        hi = (qs[:, :, k] >> 4) + np.where(qh & (2 << (2 * k)), 16, 0)
+        out[:, :, k, :32] = d1[..., None] * _f32(lo) - mm1[..., None]
+        out[:, :, k, 32:] = d2[..., None] * _f32(hi) - mm2[..., None]
+    return out.reshape(rows, cols)
+
+
+def dq_q6_k(raw: np.ndarray, cols: int) -> np.ndarray:
+    """210-byte superblocks (moelan/kernels.py:363-388): 128 ql bytes, 64 qh bytes,
+    16 int8 scales at 192, f16 d at 208. In half n (128 values), for l < 32:
+    values l, l+32, l+64, l+96 are the low nibble of ql[64n+l], of ql[64n+l+32],
+    the high nibble of ql[64n+l], of ql[64n+l+32], each with bits 2t..2t+1 of
+    qh[32n+l] as bits 4-5, minus 32; scale 8n + l//16 + 2t; w = d * (sc * q)
+    (the integer product first)."""
+    b = _blocks(raw, cols, Q6_K)
+    rows, nb = b.shape[:2]
+    d = gguf_f16(b[..., 208], b[..., 209])[..., None]
+    sc = b[..., 192:208].view(np.int8).astype(np.int32)
+    out = np.empty((rows, nb, 2, 4, 32), np.float32)
+    l = np.arange(32)
+    for n in range(2):
+        a = b[..., 64 * n:64 * n + 32].astype(np.int32)
+        c = b[..., 64 * n + 32:64 * n + 64].astype(np.int32)
+        h = b[..., 128 + 32 * n:160 + 32 * n].astype(np.int32)
+        qs = (((a & 15) | (((h >> 0) & 3) << 4)) - 32, ((c & 15) | (((h >> 2) & 3) << 4)) - 32,
+              ((a >> 4) | (((h >> 4) & 3) << 4)) - 32, ((c >> 4) | (((h >> 6) & 3) << 4)) - 32)
+        for t in range(4):
+            s_ = sc[..., 8 * n + l // 16 + 2 * t]
+            out[:, :, n, t] = d * _f32(s_ * qs[t])
+    return out.reshape(rows, cols)
+
+
 def gguf_dequant(raw: np.ndarray, qtype: int, cols: int) -> np.ndarray:
-    """moelan/kernels.py:455-476 (_gguf_row dispatch) for the two types on this path."""
-    if qtype == Q8_0:
-        return dq_q8_0(raw, cols)
-    if qtype == Q4_K:
-        return dq_q4_k(raw, cols)
-    raise ValueError(f"qtype {qtype} is not on this path")
+    """moelan/kernels.py:455-476 (_gguf_row dispatch): every quantized type."""
+    dec = {Q8_0: dq_q8_0, Q4_K: dq_q4_k, Q4_0: dq_q4_0, Q4_1: dq_q4_1, Q2_K: dq_q2_k, Q3_K: dq_q3_k,
+           Q5_K: dq_q5_k, Q6_K: dq_q6_k, Q5_0: lambda r, c: dq_q5(r, c, False),
+           Q5_1: lambda r, c: dq_q5(r, c, True)}
+    if qtype not in dec:
+        raise ValueError(f"qtype {qtype} is not a quantized GGUF type")
+    return dec[qtype](np.asarray(raw), cols)
 
 
 def gguf_matmul_t(x, raw, qtype: int, cols: int) -> np.ndarray:
@@ -169,12 +320,17 @@ def gguf_matmul_t(x, raw, qtype: int, cols: int) -> np.ndarray:
     return matmul_t_exact(x, gguf_dequant(raw, qtype, cols))
 
 
+# offsets of the f16 scale fields of each block   moelan/gguf.py:543-545
+SCALE_FIELDS = {2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 8: (0,), 10: (80, 82), 11: (108,),
+                12: (0, 2), 13: (0, 2), 14: (208,)}
+
+
 def random_blocks(rows: int, cols: int, qtype: int, rng, scale=None) -> np.ndarray:
     """Random GGUF rows with small f16 scale fields, as moelan/gguf.py:547-555
     (there a constant; ``scale`` None draws each d / dmin from |N(0, 0.01)|)."""
     _, block, size = QTYPES[qtype]
     raw = rng.integers(0, 256, (rows, cols // block, size), dtype=np.uint8)
-    fields = {8: (0,), 12: (0, 2)}[qtype]
+    fields = SCALE_FIELDS[qtype]
     for off in fields:
         if scale is None:
             v = np.abs(rng.normal(0.0, 0.01, (rows, cols // block))).astype(np.float16)

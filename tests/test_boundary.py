@@ -52,7 +52,7 @@ def test_struct_layout():
     (lambda L: L.moe_q4_matmul_t(1, 1, 1, 1, 0, 8, 63, 63, 0, 1, None), "even"),
     (lambda L: L.moe_q4_matmul_t(None, 1, 1, 1, 0, 8, 64, 32, 0, 1, None), "null pointer"),
     (lambda L: L.moe_q8_matmul_t(1, -1, 1, 1, 0, 8, 64, 32, 1, None), "n=-1"),
-    (lambda L: L.moe_gguf_matmul_t(1, 1, 1, 14, 8, 256, 1, None), "qtype 14"),
+    (lambda L: L.moe_gguf_matmul_t(1, 1, 1, 30, 8, 256, 1, None), "qtype 30"),
     (lambda L: L.moe_gguf_matmul_t(1, 1, 1, 12, 8, 100, 1, None), "multiple of 256"),
     (lambda L: L.moe_gguf_dequant(1, 8, 8, 33, 1, None), "multiple of 32"),
     (lambda L: L.moe_q4_layer(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 32, 1,
@@ -72,8 +72,16 @@ def test_bad_arguments_fail_with_a_message(call, needle):
 def test_unsupported_is_its_own_code():
     """Formats and shapes the kernels do not take report MOE_EUNSUPPORTED, not MOE_EINVAL."""
     L = _lib.lib()
-    assert L.moe_gguf_matmul_t(1, 1, 1, 14, 8, 256, 1, None) == _lib.MOE_EUNSUPPORTED
-    assert L.moe_gguf_dequant(1, 6, 8, 32, 1, None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_gguf_matmul_t(1, 1, 1, 30, 8, 256, 1, None) == _lib.MOE_EUNSUPPORTED    # BF16
+    assert L.moe_gguf_dequant(1, 9, 8, 32, 1, None) == _lib.MOE_EUNSUPPORTED            # Q8_1
+    assert L.moe_gguf_dequant(1, 1, 8, 32, 1, None) == _lib.MOE_EUNSUPPORTED            # F16
+    # rows of more than 8192 values are not taken by the block mat-vec (nothing launched)
+    assert L.moe_gguf_matmul_t(1, 1, 1, 14, 8, 256 * 33, 1, None) == _lib.MOE_EUNSUPPORTED
+    assert L.moe_gguf_matmul_t(1, 1, 1, 2, 8, 32 * 257, 1, None) == _lib.MOE_EUNSUPPORTED
+    # every quantized type is taken; its rows must hold whole blocks
+    for qt, per in ((2, 32), (3, 32), (6, 32), (7, 32), (10, 256), (11, 256), (13, 256), (14, 256)):
+        assert L.moe_gguf_matmul_t(1, 1, 1, qt, 8, per + 16, 1, None) == _lib.MOE_EINVAL
+        assert L.moe_gguf_dequant(1, qt, 8, per // 2, 1, None) == _lib.MOE_EINVAL
     assert L.moe_q4_grouped_ffn(1, 96, 1, 1, 1, 1, 4, 96, 128, 32, 1, 96, 1, 1 << 20, None) == _lib.MOE_EUNSUPPORTED
     assert "multiples of 128" in _lib.last_error()
     assert L.moe_q4_grouped_ffn(1, 128, 1, 1, 1, 1, 4, 128, 128, 16, 1, 128, 1, 1 << 20, None) == \
