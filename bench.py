@@ -303,6 +303,47 @@ def gguf_matvec(args, L, target_bytes: int = 256 << 20, cols: int = 2048):
     return res
 
 
+def wire_codec(args, L, n: int = 8192, d: int = 4096):
+    """Wire encode (moe_wire_encode) of an [n, d] f32 block in HBM (128 MB) to
+    int8 + scales and to f16, and the int8 decode back: bytes read + written
+    over HIP-event time of 20 launches each."""
+    import torch
+    stream = torch.cuda.current_stream().cuda_stream
+    a = torch.randn((n, d), device="cuda")
+    q = torch.empty((n, d), dtype=torch.int8, device="cuda")
+    h = torch.empty((n, d), dtype=torch.float16, device="cuda")
+    sc = torch.empty((n, d // 64), device="cuda")
+    back = torch.empty((n, d), device="cuda")
+    calls = {
+        "encode_int8": (lambda: L.moe_wire_encode(a.data_ptr(), d, None, n, d, 2, q.data_ptr(), sc.data_ptr(), stream),
+                        n * d * 4 + n * d + n * d // 64 * 4),
+        "encode_f16": (lambda: L.moe_wire_encode(a.data_ptr(), d, None, n, d, 1, h.data_ptr(), None, stream),
+                       n * d * 4 + n * d * 2),
+        "decode_int8": (lambda: L.moe_wire_decode(q.data_ptr(), sc.data_ptr(), 2, n, d, None, back.data_ptr(), d,
+                                                  stream), n * d + n * d // 64 * 4 + n * d * 4),
+    }
+    res = {}
+    for name, (fn, byts) in calls.items():
+        for _ in range(3):
+            if fn():
+                from distributedmoellm_amd import _lib
+                raise RuntimeError(_lib.last_error())
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(20):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) / 20 * 1e3
+        res[name] = dict(us=round(us, 2), bytes=byts, gbs=round(byts / us / 1e3, 1),
+                         hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4))
+        log(f"wire {name}: {us:.1f} us, {byts / us / 1e3:.0f} GB/s")
+    res["workload"] = f"[{n}, {d}] f32 activations in HBM (128 MB), 20 launches each"
+    del a, q, h, sc, back
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline_decode(seconds: float = 12.0):
     """The reference's fused layer kernel restated in C/OpenMP (oracle/cpuref.c)
     on the host cores: one token's 384 experts per call from a pool of 64
@@ -495,7 +536,7 @@ def main() -> int:
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, prefill, copy "
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, wire, prefill, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -523,6 +564,8 @@ def main() -> int:
             res["decode_i8"] = decode384_gs64(args, L)
         if "gguf" in only:
             res["gguf"] = gguf_matvec(args, L)
+        if "wire" in only:
+            res["wire"] = wire_codec(args, L)
         if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
             import torch
             a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -544,6 +587,7 @@ def main() -> int:
         extras["per_layer_calls"] = r.pop("per_layer_calls")
     extras["decode384_gs64"] = decode384_gs64(args, L)
     extras["gguf_matvec"] = gguf_matvec(args, L)
+    extras["wire"] = wire_codec(args, L)
     if args.stack:
         extras["stack_235b"] = stack_decode(args, L)
     log("prefill (Qwen3-30B-A3B layer, T=512) ...")

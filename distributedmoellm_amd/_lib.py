@@ -66,6 +66,8 @@ SIGNATURES = {
     "moe_q4_layer_i8": (c_int, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I,
                                 _I, _I, _I, _I, _P, _Z, _P]),
     "moe_round_q8": (c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P]),
+    "moe_wire_encode": (c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    "moe_wire_decode": (c_int, [_P, _P, _I, _I, _I, _P, _P, _I, _P]),
 }
 
 _lib = None

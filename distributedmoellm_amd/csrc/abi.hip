@@ -11,6 +11,7 @@
 #include "layer.h"
 #include "matvec.h"
 #include "prefill.h"
+#include "wire.h"
 
 static_assert(sizeof(moe_q4_expert) == sizeof(moe::ExpertDesc), "moe_q4_expert layout");
 static_assert(offsetof(moe_q4_expert, xor8) == offsetof(moe::ExpertDesc, xor8), "moe_q4_expert layout");
@@ -287,6 +288,30 @@ MOE_API int moe_round_q8(const float* x, int ldx, const int* xrow, int n, int K,
   REQUIRE(ldx >= K, "moe_round_q8: ldx=%d must be >= K=%d", ldx, K);
   REQUIRE(x && q && d && s8, "moe_round_q8: null pointer");
   return run_round_q8(x, ldx, xrow, n, K, 0, gs, q, d, s8, as_stream(stream));
+}
+
+// ------------------------------------------------------------------ wire format
+
+MOE_API int moe_wire_encode(const float* a, int lda, const int* rows, int n, int d, int wire, void* out, float* scale,
+                            void* stream) {
+  REQUIRE(wire == MOE_WIRE_F32 || wire == MOE_WIRE_F16 || wire == MOE_WIRE_INT8,
+          "moe_wire_encode: wire format %d (0 f32, 1 f16, 2 int8)", wire);
+  REQUIRE(n >= 0 && d > 0, "moe_wire_encode: n=%d d=%d", n, d);
+  if (n == 0) return MOE_OK;
+  REQUIRE(lda >= d, "moe_wire_encode: lda=%d must be >= d=%d", lda, d);
+  REQUIRE(a && out && (wire != MOE_WIRE_INT8 || scale), "moe_wire_encode: null pointer");
+  return run_wire_encode(a, lda, rows, n, d, wire, out, scale, as_stream(stream));
+}
+
+MOE_API int moe_wire_decode(const void* in, const float* scale, int wire, int n, int d, const int* rows, float* out,
+                            int ldo, void* stream) {
+  REQUIRE(wire == MOE_WIRE_F32 || wire == MOE_WIRE_F16 || wire == MOE_WIRE_INT8,
+          "moe_wire_decode: wire format %d (0 f32, 1 f16, 2 int8)", wire);
+  REQUIRE(n >= 0 && d > 0, "moe_wire_decode: n=%d d=%d", n, d);
+  if (n == 0) return MOE_OK;
+  REQUIRE(ldo >= d, "moe_wire_decode: ldo=%d must be >= d=%d", ldo, d);
+  REQUIRE(in && out && (wire != MOE_WIRE_INT8 || scale), "moe_wire_decode: null pointer");
+  return run_wire_decode(in, scale, wire, n, d, rows, out, ldo, as_stream(stream));
 }
 
 MOE_API int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, void* stream) {

@@ -170,6 +170,27 @@ int moe_q4_layer_i8(const float* x, int ldx, const moe_q4_expert* table, const i
 int moe_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int gs, int8_t* q, float* d, int32_t* s8,
                  void* stream);
 
+/* ------------------------------------------------------------ wire format */
+
+/* Activations between a coordinator and its workers (moelan/protocol.py:90-123). */
+#define MOE_WIRE_F32 0
+#define MOE_WIRE_F16 1
+#define MOE_WIRE_INT8 2
+
+/* Rows rows[r] (rows NULL: r) of a [*, lda], r < n, encoded as encode_rows
+ * (moelan/protocol.py:99-114) into out [n, d]: f32 (a copy), f16 (round to
+ * nearest even, as numpy's astype), or int8 with scale [n, d/gs] f32, gs = 64
+ * when 64 divides d, else d: s = max|g| / 127 (1 for a zero group),
+ * q = clip(rint(g / s), -127, 127). Bit-exact for finite inputs. The worker
+ * encodes y[touched] this way (moelan/worker.py:352-354). */
+int moe_wire_encode(const float* a, int lda, const int* rows, int n, int d, int wire, void* out, float* scale,
+                    void* stream);
+
+/* Row r of in [n, d] decoded (decode_rows, moelan/protocol.py:116-123: q * s
+ * for int8) into out[rows[r]] (rows NULL: out[r]), row stride ldo. */
+int moe_wire_decode(const void* in, const float* scale, int wire, int n, int d, const int* rows, float* out, int ldo,
+                    void* stream);
+
 /* ------------------------------------------------ prompt reading (prefill) */
 
 /* Bytes of workspace that let moe_router_logits split H over more workgroups. */

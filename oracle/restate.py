@@ -340,6 +340,41 @@ def random_blocks(rows: int, cols: int, qtype: int, rng, scale=None) -> np.ndarr
     return raw.reshape(rows, cols // block * size)
 
 
+# ------------------------------------------------------------------ wire format
+
+WIRE_GROUP = 64
+
+
+def wire_encode(a, wire: str):
+    """encode_rows (moelan/protocol.py:99-114) in numpy: f16 by numpy's cast (round
+    to nearest even); int8 per row in groups of 64 values (the whole row when 64
+    does not divide it): s = max|g| / 127 in f32 (1 where that is 0), q =
+    clip(rint(g / s), -127, 127) with rint rounding half to even. Returns the
+    wire array, and for int8 also the (n, d / gs) f32 scales."""
+    a = np.asarray(a, np.float32)
+    if wire == "f16":
+        with np.errstate(over="ignore"):
+            return a.astype(np.float16)
+    if wire == "f32":
+        return a.copy()
+    n, d = a.shape
+    gs = WIRE_GROUP if d % WIRE_GROUP == 0 else d
+    g = a.reshape(n, d // gs, gs)
+    sc = (np.abs(g).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    sc[sc == 0] = np.float32(1.0)
+    q = np.clip(np.rint((g / sc[:, :, None]).astype(np.float32)), -127, 127).astype(np.int8)
+    return q.reshape(n, d), sc
+
+
+def wire_decode(q, sc=None) -> np.ndarray:
+    """decode_rows (moelan/protocol.py:116-123): q * s in f32 for int8, else a cast."""
+    q = np.asarray(q)
+    if q.dtype == np.int8:
+        n, d = q.shape
+        return (q.reshape(n, sc.shape[1], -1).astype(np.float32) * np.asarray(sc, np.float32)[:, :, None]).reshape(n, d)
+    return q.astype(np.float32)
+
+
 # ------------------------------------------------------------------ experts
 
 def silu(x):

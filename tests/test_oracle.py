@@ -341,3 +341,47 @@ def test_moe_q4i_close_to_float_layer():
     for r in range(6):
         if np.abs(want[r]).max() > 0:
             assert np.linalg.norm(got[r] - want[r]) < 5e-2 * np.linalg.norm(want[r])
+
+
+# ---------------------------------------------------------------- wire format
+
+def test_wire_int8_known_answers():
+    """encode_rows int8 (moelan/protocol.py:104-110) pinned by what it must do: a
+    group whose largest |v| is 127 has scale exactly 1, so q = rint(v) with ties
+    to even (2.5 -> 2, 3.5 -> 4, -2.5 -> -2); a zero group has scale 1 and q 0;
+    rows whose width 64 does not divide take one scale for the whole row."""
+    a = np.zeros((2, 128), np.float32)
+    a[0, :6] = [127.0, 2.5, 3.5, -2.5, 0.5, -127.0]
+    q, s = R.wire_encode(a, "int8")
+    assert s.shape == (2, 2) and s[0, 0] == 1.0 and s[0, 1] == 1.0 and s[1, 0] == 1.0
+    assert q[0, :6].tolist() == [127, 2, 4, -2, 0, -127]
+    assert (q[1] == 0).all()
+    b = np.zeros((1, 96), np.float32)
+    b[0, 0], b[0, 95] = 254.0, -1.0
+    q, s = R.wire_encode(b, "int8")
+    assert s.shape == (1, 1) and s[0, 0] == np.float32(2.0)
+    assert q[0, 0] == 127 and q[0, 95] == 0          # -0.5 rounds to even 0
+
+
+def test_wire_int8_error_bound_and_range():
+    """decode(encode(a)) is within half a step of a, every |q| <= 127 and each
+    group's largest |v| maps to +-127."""
+    rng = np.random.default_rng(40)
+    a = (rng.standard_normal((9, 256)) * rng.uniform(1e-3, 1e3, (9, 1))).astype(np.float32)
+    q, s = R.wire_encode(a, "int8")
+    back = R.wire_decode(q, s)
+    err = np.abs(back - a).reshape(9, 4, 64)
+    assert (err <= s[:, :, None] * 0.5 * (1 + 1e-6)).all()
+    assert (np.abs(q.reshape(9, 4, 64)).max(axis=2) == 127).all()
+
+
+def test_wire_f16_rounding():
+    """f16 on the wire is numpy's cast: round to nearest even, overflow past
+    65520 to inf, gradual underflow."""
+    v = np.array([65504.0, 65519.0, 65520.0, 1 + 2 ** -11, 1 + 3 * 2 ** -11, 2 ** -24, 2 ** -25,
+                  3 * 2 ** -26, -0.0], np.float32)
+    h = R.wire_encode(v[None, :], "f16")[0].astype(np.float64)
+    assert h[0] == 65504 and h[1] == 65504 and np.isinf(h[2])
+    assert h[3] == 1.0 and h[4] == 1 + 2 ** -9
+    assert h[5] == 2 ** -24 and h[6] == 0 and h[7] == 2 ** -24
+    assert np.signbit(h[8])

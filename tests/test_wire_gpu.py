@@ -1,0 +1,126 @@
+"""Activations on the wire, encoded and decoded on the GPU (moelan/protocol.py:
+90-123), and the worker's moe step (moelan/worker.py:337-354): bit-exact with
+the oracle's encode_rows / decode_rows for finite inputs."""
+
+import numpy as np
+import pytest
+import torch
+
+from distributedmoellm_amd import experts as X
+from distributedmoellm_amd import wire as W
+from oracle import restate as R
+
+pytestmark = pytest.mark.gpu
+
+
+def rows_of(rng, n, d):
+    a = (rng.standard_normal((n, d)) * rng.choice([1e-4, 1.0, 3e3], (n, 1))).astype(np.float32)
+    a[0, :64] = 0.0                                      # a zero group
+    a[1, :64] = np.arange(-32, 32) + 0.5                 # halves at scale != 1
+    a[1, 64:128] = 0.0
+    a[1, 64] = 127.0
+    a[1, 65:70] = [2.5, 3.5, -2.5, -0.5, 0.5]            # ties at scale exactly 1
+    return a
+
+
+@pytest.mark.parametrize("d", [2048, 768, 96, 1])
+def test_int8_encode_bit_exact(kernels, d):
+    rng = np.random.default_rng(d)
+    a = rows_of(rng, 7, max(d, 128))[:, :d] if d >= 128 else rng.standard_normal((7, d)).astype(np.float32)
+    got = W.encode_rows(a, "int8", "y")
+    q, s = R.wire_encode(a, "int8")
+    assert np.array_equal(got["y"], q)
+    assert np.array_equal(got["y_scale"].view(np.uint32), s.view(np.uint32))
+    back = W.decode_rows(got, "y")
+    assert np.array_equal(back.view(np.uint32), R.wire_decode(q, s).view(np.uint32))
+
+
+def test_f16_encode_bit_exact(kernels):
+    rng = np.random.default_rng(3)
+    a = rows_of(rng, 5, 512)
+    a[2, :9] = [65504.0, 65519.0, 65520.0, 1 + 2 ** -11, 1 + 3 * 2 ** -11, 2 ** -24, 2 ** -25, 3 * 2 ** -26, -0.0]
+    a[3, :4] = [1e-30, -1e-30, 7e4, -7e4]
+    got = W.encode_rows(a, "f16", "x")
+    want = R.wire_encode(a, "f16")
+    assert np.array_equal(got["x"].view(np.uint16), want.view(np.uint16))
+    assert np.array_equal(W.decode_rows(got, "x"), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("wire", ["f32", "f16", "int8"])
+def test_encode_gathers_rows_on_the_device(kernels, wire):
+    """The worker encodes y[touched] (moelan/worker.py:352-354) without a host pass."""
+    rng = np.random.default_rng(5)
+    y = torch.from_numpy(rows_of(rng, 40, 2048)).cuda()
+    touched = np.array([0, 1, 3, 17, 39], np.int32)
+    got = W.encode_rows(y, wire, "y", rows=touched)
+    assert all(v.is_cuda for v in got.values())
+    want = R.wire_encode(y.cpu().numpy()[touched], wire)
+    if wire == "int8":
+        assert np.array_equal(got["y"].cpu().numpy(), want[0])
+        assert np.array_equal(got["y_scale"].cpu().numpy(), want[1])
+    else:
+        assert np.array_equal(got["y"].cpu().numpy().view(np.uint8), want.view(np.uint8))
+    # decode scatters the rows back into a strided f32 output
+    out = torch.zeros((40, 2056), device="cuda")[:, :2048]
+    W.decode_rows({k: v for k, v in got.items()}, "y", out=out, rows=touched)
+    back = R.wire_decode(*want) if wire == "int8" else want.astype(np.float32)
+    o = out.cpu().numpy()
+    assert np.array_equal(o[touched], back)
+    assert not np.delete(o, touched, axis=0).any()
+
+
+@pytest.mark.parametrize("wire", ["f32", "f16", "int8"])
+def test_worker_moe_step(kernels, wire):
+    """x in the wire format in, the store's layer call, y's touched rows out."""
+    rng = np.random.default_rng(7)
+    H, I = 256, 128
+    experts = {(0, e): X.synthetic_expert(H, I, "int4", 32, rng) for e in range(6)}
+    store = X.ExpertStore(experts, fmt="int4")
+    x = rng.standard_normal((5, H)).astype(np.float32)
+    sel = [(1, [0, 2]), (3, [2]), (4, [0, 2, 4]), (5, [4])]
+    ex = np.array([e for e, _ in sel], np.int32)
+    rows = np.concatenate([np.array(r, np.int32) for _, r in sel])
+    off = np.concatenate([[0], np.cumsum([len(r) for _, r in sel])]).astype(np.int32)
+    w = rng.random(len(rows)).astype(np.float32)
+    arrays = dict(W.encode_rows(x, "f32", "x"), experts=ex, offsets=off, rows=rows, weights=w)
+    reply = W.worker_moe(store, 0, arrays, wire)
+    assert reply["rows"].tolist() == [0, 2, 4]
+    groups = [(e, np.array(r), w[off[i]:off[i + 1]]) for i, (e, r) in enumerate(sel)]
+    exact = R.store_compute(x, groups, lambda e, xr: R.expert_exact(
+        xr, R.q4_dequant64(experts[(0, e)].gu.raw, experts[(0, e)].gu.s, 32, False),
+        R.q4_dequant64(experts[(0, e)].down.raw, experts[(0, e)].down.s, 32, False), I))[[0, 2, 4]]
+    y = W.decode_rows({k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v) for k, v in reply.items()}, "y")
+    step = np.abs(exact).reshape(3, -1, 64).max(axis=2, keepdims=True) / 127
+    tol = {"f32": 1e-5 * np.abs(exact).max(), "f16": 1e-3 * np.abs(exact),
+           "int8": np.broadcast_to(step * 0.5001 + 1e-5 * np.abs(exact).max(), (3, H // 64, 64)).reshape(3, H)}[wire]
+    assert (np.abs(y - exact) <= tol + 1e-7).all()
+
+
+@pytest.mark.parametrize("wire", [0, 1, 2])
+def test_unaligned_rows_take_the_scalar_kernels(kernels, wire):
+    """Rows an odd number of values apart (no 16-byte loads): same bytes."""
+    from distributedmoellm_amd import _lib
+    rng = np.random.default_rng(11 + wire)
+    n, d = 6, 256
+    full = torch.from_numpy(rows_of(rng, n, d + 1)).cuda()          # lda = 257
+    dt = {0: torch.float32, 1: torch.float16, 2: torch.int8}[wire]
+    out = torch.empty((n, d), dtype=dt, device="cuda")
+    sc = torch.empty((n, d // 64), device="cuda")
+    rows = torch.tensor([5, 0, 3, 1, 2, 4], dtype=torch.int32, device="cuda")
+    L = _lib.lib()
+    assert L.moe_wire_encode(full.data_ptr(), d + 1, rows.data_ptr(), n, d, wire, out.data_ptr(), sc.data_ptr(),
+                             torch.cuda.current_stream().cuda_stream) == 0
+    src = full.cpu().numpy()[[5, 0, 3, 1, 2, 4], :d]
+    want = R.wire_encode(src, {0: "f32", 1: "f16", 2: "int8"}[wire])
+    if wire == 2:
+        assert np.array_equal(out.cpu().numpy(), want[0]) and np.array_equal(sc.cpu().numpy(), want[1])
+    else:
+        assert np.array_equal(out.cpu().numpy().view(np.uint8), want.view(np.uint8))
+    # decode into rows 1 value apart from 16-byte alignment
+    dst = torch.zeros((n, d + 1), device="cuda")
+    assert L.moe_wire_decode(out.data_ptr(), sc.data_ptr(), wire, n, d, None, dst.data_ptr() + 4, d + 1,
+                             torch.cuda.current_stream().cuda_stream) == 0
+    back = R.wire_decode(*want) if wire == 2 else want.astype(np.float32)
+    flat = dst.cpu().numpy().reshape(-1)
+    got = flat[1 + np.arange(n)[:, None] * (d + 1) + np.arange(d)[None, :]]
+    assert np.array_equal(got, back)
