@@ -344,6 +344,59 @@ def wire_codec(args, L, n: int = 8192, d: int = 4096):
     return res
 
 
+def residency(args, L, n: int = 64):
+    """Experts from a colibri int4 container into HBM: n experts of the
+    Qwen3-30B-A3B shape (H=2048, I=768, group 32, f32 scales as colibri stores
+    them) written to a temporary directory (so in the page cache), then
+    ExpertStore.pin of all of them timed: memory-mapped views, one
+    host-to-device copy per array. Bound by the host link, not HBM."""
+    import json as _json
+    import tempfile
+    import torch
+    from safetensors.numpy import save_file
+    from distributedmoellm_amd import experts as X
+    from distributedmoellm_amd import sources as S
+    H, I, gs = 2048, 768, 32
+    rng = np.random.default_rng(9)
+    with tempfile.TemporaryDirectory() as d:
+        tensors = {}
+        for e in range(n):
+            p = f"model.layers.0.mlp.experts.{e}"
+            tensors[f"{p}.merged_weight"] = rng.integers(0, 256, 3 * H * I // 2, dtype=np.uint8)
+            tensors[f"{p}.qs"] = rng.random(3 * H * I // gs, dtype=np.float32)
+        save_file(tensors, f"{d}/model.safetensors")
+        del tensors
+        with open(f"{d}/config.json", "w") as f:
+            _json.dump({"model_type": "qwen3_moe", "hidden_size": H, "moe_intermediate_size": I, "num_experts": n,
+                        "num_hidden_layers": 1}, f)
+        with open(f"{d}/qwen36_meta.json", "w") as f:
+            _json.dump({"ebits": 4, "expert_gs": gs}, f)
+        src = S.CheckpointSource(d)
+        X.ExpertStore([src]).pin([(0, 0)])           # the staging buffers and the copy path
+        torch.cuda.synchronize()
+        keys = [(0, e) for e in range(n)]
+        times = []
+        for _ in range(2):   # first into new device memory, then again after forget (memory torch keeps)
+            store = X.ExpertStore([src])
+            t0 = time.perf_counter()
+            store.pin(keys)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            byts = store.resident_bytes()
+            store.forget(keys)
+            del store
+        del src
+    torch.cuda.empty_cache()
+    res = dict(experts=n, bytes=byts, seconds=round(times[0], 4), gbs=round(byts / times[0] / 1e9, 2),
+               seconds_warm=round(times[1], 4), gbs_warm=round(byts / times[1] / 1e9, 2), bound="host link",
+               workload=f"{n} colibri int4 experts (H=2048 I=768 gs=32, f32 scales, {byts / 1e6:.0f} MB) "
+                        "pinned from a page-cached container; gbs into new device memory, gbs_warm into "
+                        "memory the allocator already holds")
+    log(f"residency: {n} experts, {byts / 1e6:.0f} MB in {times[0] * 1e3:.1f} ms = {res['gbs']} GB/s "
+        f"(again: {times[1] * 1e3:.1f} ms = {res['gbs_warm']} GB/s)")
+    return res
+
+
 def cpu_baseline_decode(seconds: float = 12.0):
     """The reference's fused layer kernel restated in C/OpenMP (oracle/cpuref.c)
     on the host cores: one token's 384 experts per call from a pool of 64
@@ -536,7 +589,7 @@ def main() -> int:
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, wire, prefill, copy "
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, wire, residency, prefill, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -566,6 +619,8 @@ def main() -> int:
             res["gguf"] = gguf_matvec(args, L)
         if "wire" in only:
             res["wire"] = wire_codec(args, L)
+        if "residency" in only:
+            res["residency"] = residency(args, L)
         if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
             import torch
             a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -588,6 +643,7 @@ def main() -> int:
     extras["decode384_gs64"] = decode384_gs64(args, L)
     extras["gguf_matvec"] = gguf_matvec(args, L)
     extras["wire"] = wire_codec(args, L)
+    extras["residency"] = residency(args, L)
     if args.stack:
         extras["stack_235b"] = stack_decode(args, L)
     log("prefill (Qwen3-30B-A3B layer, T=512) ...")

@@ -16,7 +16,7 @@ import numpy as np
 
 from . import kernels
 
-FORMATS = ("int8", "int4", "native")
+FORMATS = ("int8", "int4", "native")   # resident formats (moelan/experts.py: FORMATS)
 
 
 def _dev_or_none(a):
@@ -51,6 +51,11 @@ class GroupQuant:
             self._dev = (kernels.to_device(self.q, torch.int8).reshape(O, I),
                          kernels.to_device(self.s).reshape(O, I // self.gs))
         return self._dev
+
+    def host_arrays(self):
+        """The host arrays device_arrays() uploads, with their device shapes."""
+        O, I = self.q.shape
+        return [(self.q, (O, I)), (self.s, (O, I // self.gs))]
 
     @property
     def shape(self):
@@ -91,6 +96,11 @@ class Packed4:
             self._dev = (kernels.to_device(self.raw, torch.uint8).reshape(O, I // 2),
                          kernels.to_device(self.s).reshape(O, I // self.gs))
         return self._dev
+
+    def host_arrays(self):
+        """The host arrays device_arrays() uploads, with their device shapes."""
+        O, I = self.shape
+        return [(self.raw, (O, I // 2)), (self.s, (O, I // self.gs))]
 
     def resident(self) -> "Packed4":
         """A copy in offset form (moelan/experts.py:188-191), XOR-ed once on the
@@ -193,33 +203,238 @@ def synthetic_expert(hidden: int, inter: int, fmt: str, gs: int = 32, rng=None, 
     return Expert(mat(2 * inter, hidden), mat(hidden, inter), inter)
 
 
-class ExpertStore:
-    """Resident experts by (layer, expert) and the per-layer compute call
-    (moelan/experts.py:538-670, the compute path only: no disk tiers)."""
+def _matrices(e: Expert):
+    for m in (e.gu, e.down):
+        yield from getattr(m, "parts", (m,))
 
-    def __init__(self, experts: dict | None = None, fmt: str = "int4"):
+
+_TORCH_OF = {np.dtype(np.uint8): "uint8", np.dtype(np.int8): "int8", np.dtype(np.float16): "float16",
+             np.dtype(np.float32): "float32"}
+
+
+_STAGES: dict = {}   # staging bytes -> two pinned host buffers, kept for the process
+
+
+def _staging(stage_bytes: int):
+    """Two pinned host buffers of ``stage_bytes``, made once and written
+    through once (first writes to new pinned pages run at a fraction of the
+    speed of later ones)."""
+    import torch
+    st = _STAGES.get(stage_bytes)
+    if st is None:
+        bufs = [torch.empty(stage_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        views = [b.numpy() for b in bufs]
+        for v in views:
+            v.fill(0)
+        st = _STAGES[stage_bytes] = (bufs, views)
+    return st
+
+
+def upload_experts(experts, stage_bytes: int = 32 << 20) -> None:
+    """Device copies of many experts' matrices in few transfers: the matrices
+    are packed (256-byte aligned) into a pinned staging buffer, which goes to
+    one device allocation in one asynchronous copy; each matrix keeps views
+    of that allocation (it is freed when the last of them goes). Two staging
+    buffers alternate, so packing the next batch out of the (memory-mapped)
+    source overlaps the transfer of the last. Matrices already on the device,
+    or larger than a staging buffer, take device_arrays(). Not thread-safe:
+    the staging buffers are shared by every call in the process."""
+    import torch
+    todo = []
+    for e in experts:
+        for part in _matrices(e):
+            if getattr(part, "_dev", None) is not None or not hasattr(part, "host_arrays"):
+                continue
+            arrs = part.host_arrays()
+            if any(kernels.is_device(a) or np.asarray(a).dtype not in _TORCH_OF for a, _ in arrs):
+                part.device_arrays()
+                continue
+            todo.append((part, arrs))
+    if not todo:
+        return
+    dev = kernels.device()
+    stages, views = _staging(stage_bytes)
+    done = [None, None]
+    slot, used, batch = 0, 0, []
+
+    def flush():
+        # host copies of the batch in parallel pieces (numpy drops the GIL), then its transfers
+        pieces = []
+        for part, arrs, offs, total, base in batch:
+            for (a, _), off in zip(arrs, offs):
+                b = np.asarray(a).reshape(-1).view(np.uint8)
+                for lo in range(0, b.size, 4 << 20):
+                    pieces.append((views[slot][base + off + lo:base + off + min(b.size, lo + (4 << 20))],
+                                   b[lo:lo + (4 << 20)]))
+        list(_copy_pool().map(lambda p: np.copyto(p[0], p[1]), pieces))
+        if not batch:
+            return
+        # one device allocation and one transfer for the batch; each matrix keeps views of it
+        n = batch[-1][4] + batch[-1][3]
+        d = torch.empty(n, dtype=torch.uint8, device=dev)
+        d.copy_(stages[slot][:n], non_blocking=True)
+        for part, arrs, offs, total, base in batch:
+            part._dev = tuple(d[base + off:base + off + np.asarray(a).nbytes]
+                              .view(getattr(torch, _TORCH_OF[np.asarray(a).dtype])).reshape(shape)
+                              for (a, shape), off in zip(arrs, offs))
+        batch.clear()
+
+    for part, arrs in todo:
+        offs, total = [], 0
+        for a, _ in arrs:
+            offs.append(total)
+            total += (np.asarray(a).nbytes + 255) // 256 * 256
+        if total > stage_bytes:
+            part.device_arrays()
+            continue
+        if used + total > stage_bytes:            # switch buffers; wait until the other one is free
+            flush()
+            done[slot] = torch.cuda.Event()
+            done[slot].record()
+            slot, used = slot ^ 1, 0
+            if done[slot] is not None:
+                done[slot].synchronize()
+        batch.append((part, arrs, offs, total, used))
+        used += total
+    flush()
+    torch.cuda.current_stream().synchronize()     # the staging buffers are free again
+
+
+_POOL = None
+
+
+def _copy_pool():
+    global _POOL
+    if _POOL is None:
+        from concurrent.futures import ThreadPoolExecutor
+        _POOL = ThreadPoolExecutor(8, thread_name_prefix="moehip-stage")
+    return _POOL
+
+
+def to_format(e: Expert, fmt: str) -> Expert:
+    """An expert in a resident format (moelan/experts.py:276-301): ``native``
+    keeps the file's encoding; ``int4`` keeps colibri's bytes as they are (the
+    kernels read them with their XOR); ``int8`` widens int4 nibbles to int8."""
+    if fmt == "native":
+        return e
+
+    def conv(m):
+        if fmt == "int4":
+            if isinstance(m, Packed4):
+                return m
+            raise ValueError("int4 residency needs an int4 checkpoint (e.g. a colibri container)")
+        if isinstance(m, Packed4):
+            return m.to_int8()
+        if isinstance(m, GroupQuant):
+            return m
+        raise ValueError(f"int8 residency of a {type(m).__name__} matrix is not provided")
+    return Expert(conv(e.gu), conv(e.down), e.inter)
+
+
+class ExpertStore:
+    """Experts by (layer, expert) in HBM and the per-layer compute call
+    (moelan/experts.py:538-670).
+
+    Tiers, as the reference's (HBM where it has RAM):
+    - ``pinned``: uploaded by :meth:`pin`, kept until unpinned;
+    - ``lru``: experts read on demand from a source that copies, at most
+      ``lru_size`` (0: none kept);
+    - ``mapped``: experts read on demand as views of a memory-mapped file
+      (``zero_copy`` sources), at most ``map_size``; each keeps the device
+      copy it made on first use while it is listed.
+    Hits count pinned and LRU experts, misses the others (as the reference).
+    ``sources`` may also be a dict {(layer, expert): Expert} of experts to pin.
+    """
+
+    def __init__(self, sources=None, fmt: str = "int4", lru_size: int = 0, map_size: int = 4096):
+        from collections import OrderedDict
         if fmt not in FORMATS:
             raise ValueError(f"format must be one of {FORMATS}")
         self.fmt = fmt
-        self.pinned: dict = dict(experts or {})
+        self.lru_size, self.map_size = lru_size, map_size
+        self.pinned: dict = {}
+        self.lru: OrderedDict = OrderedDict()
+        self.mapped: OrderedDict = OrderedDict()
         self.hits = 0
         self.misses = 0
+        if isinstance(sources, dict):
+            self.sources = []
+            self.pinned.update({tuple(k): e for k, e in sources.items()})
+        else:
+            self.sources = [s for s in (sources or []) if s is not None]
+
+    def _read_from(self, key, fmt: str | None = None):
+        for src in self.sources:
+            if src.has(key):
+                e = src.load(key)
+                return (to_format(e, fmt) if fmt else e), src
+        raise KeyError(f"expert {key} is not available on this node")
+
+    def can_serve(self, key) -> bool:
+        key = tuple(key)
+        return key in self.pinned or any(s.has(key) for s in self.sources)
 
     def pin(self, items) -> None:
-        """Add experts ((layer, expert), Expert) and upload their arrays now."""
-        for key, e in items:
-            for m in (e.gu, e.down):
-                for part in getattr(m, "parts", (m,)):
-                    if hasattr(part, "device_arrays"):
-                        part.device_arrays()
-            self.pinned[tuple(key)] = e
+        """Pin experts and upload their arrays now: keys (read from the
+        sources, moelan/experts.py:581-590) or ((layer, expert), Expert) pairs."""
+        new = []
+        for it in items:
+            if len(it) == 2 and isinstance(it[1], Expert):
+                key, e = tuple(it[0]), it[1]
+            else:
+                key = tuple(it)
+                if key in self.pinned:
+                    continue
+                e = self.lru.pop(key, None) or self.mapped.pop(key, None) or self._read_from(key, self.fmt)[0]
+            self.pinned[key] = e
+            new.append(e)
+        upload_experts(new)
+
+    def unpin_all_except(self, keep) -> None:
+        keep = {tuple(k) for k in keep}
+        for key in list(self.pinned):
+            if key not in keep:
+                del self.pinned[key]
+
+    def forget(self, keys) -> None:
+        """Drop every reference to ``keys`` (their device copies go with them)."""
+        for k in keys:
+            k = tuple(k)
+            self.pinned.pop(k, None)
+            self.lru.pop(k, None)
+            self.mapped.pop(k, None)
 
     def get(self, key):
-        e = self.pinned.get(tuple(key))
-        if e is None:
-            raise KeyError(f"expert {key} is not resident")
-        self.hits += 1
+        """The expert for ``key`` (moelan/experts.py:610-635)."""
+        key = tuple(key)
+        e = self.pinned.get(key)
+        if e is not None:
+            self.hits += 1
+            return e
+        e = self.lru.get(key)
+        if e is not None:
+            self.lru.move_to_end(key)
+            self.hits += 1
+            return e
+        e = self.mapped.get(key)
+        if e is not None:
+            self.mapped.move_to_end(key)
+            self.misses += 1
+            return e
+        self.misses += 1
+        e, src = self._read_from(key)
+        if getattr(src, "zero_copy", False):
+            self.mapped[key] = e
+            while len(self.mapped) > self.map_size:
+                self.mapped.popitem(last=False)
+        elif self.lru_size > 0:
+            self.lru[key] = e
+            while len(self.lru) > self.lru_size:
+                self.lru.popitem(last=False)
         return e
+
+    def resident_bytes(self) -> int:
+        return sum(e.nbytes for e in self.pinned.values()) + sum(e.nbytes for e in self.lru.values())
 
     def compute(self, layer: int, x, groups, mfma: bool = True):
         """Weighted sum of the routed experts' outputs for the given rows

@@ -59,6 +59,10 @@ class QuantMatrix:
             self._dev = (kernels.to_device(self.raw, torch.uint8).reshape(self.raw.shape[0], -1),)
         return self._dev
 
+    def host_arrays(self):
+        """The host array device_arrays() uploads, with its device shape."""
+        return [(self.raw, (self.raw.shape[0], -1))]
+
     def matmul_t(self, x):
         return kernels.gguf_matmul_t(x, self.device_arrays()[0], self.qtype, self.shape[1])
 
