@@ -32,7 +32,7 @@ int run_q4i8_layer(const Q4LayerArgs& a, hipStream_t st);
 int run_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, hipStream_t st);
 int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
                 float* out, int ldo, int H, hipStream_t st);
-// the same sum in runs of pairs (two launches, y overwritten); max_pairs bounds a row's pairs
+// the same sum in one launch: a block per (row, 16 columns), 64 pair lanes added by a fixed tree
 int run_combine_runs(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
                      int max_pairs, float* out, int ldo, int H, hipStream_t st);
 

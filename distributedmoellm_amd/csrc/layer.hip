@@ -72,93 +72,67 @@ int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const
   return check_launch("weighted combine");
 }
 
-// The layer call's combine, in two launches, for rows with many pairs (one
-// token's 384 experts): the pair list of a row is cut into runs of kRun pairs
-// in list order. Launch 1: a block sums one run for 1024 columns (a thread
-// takes 4 columns, its kRun loads issued together) and writes the partial sum
-// over the y row of the run's first pair, which no other block reads (each
-// pair belongs to one row and one run); a row with a single run is added to
-// out at once. Launch 2: per row of more than one run, the partial sums in
-// run order, added to out. Fixed order, no atomics. y is overwritten.
-constexpr int kRun = 8;
-
-__global__ __launch_bounds__(256) void combine_runs_kernel(float* y, int ldy, const float* pw, const int* rrow,
+// One launch: a block takes 16 columns of one row, 4 threads per column
+// quad x 64 pair lanes; lane j sums the row's pairs j, j+64, j+128, ... in
+// list order (their loads issued together), then the 64 lane sums are added
+// by a fixed binary tree in LDS and the total goes to out. Fixed order, no
+// atomics; y is only read.
+__global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int ldy, const float* pw, const int* rrow,
                                                            const int* rptr, const int* rpair, int nr, float* out,
                                                            int ldo, int H) {
-  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
-  if (c >= H) return;
+  __shared__ float4 red[64][4];
+  const int q = threadIdx.x & 3, j = threadIdx.x >> 2;
+  const int c = blockIdx.x * 16 + q * 4;
   for (int i = blockIdx.y; i < nr; i += gridDim.y) {
     const int r0 = rptr[i], r1 = rptr[i + 1];
-    for (int q0 = r0 + blockIdx.z * kRun; q0 < r1; q0 += gridDim.z * kRun) {
-      const int n = min(kRun, r1 - q0);
-      int ps[kRun];
-      float ws[kRun];
-      float4 v[kRun];
-#pragma unroll
-      for (int j = 0; j < kRun; ++j) {
-        ps[j] = rpair[q0 + (j < n ? j : 0)];
-        ws[j] = j < n ? pw[ps[j]] : 0.f;
-        v[j] = *reinterpret_cast<const float4*>(y + (size_t)ps[j] * ldy + c);
-      }
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int j = 0; j < kRun; ++j) {
-        if (j < n) {
-          a.x += ws[j] * v[j].x;
-          a.y += ws[j] * v[j].y;
-          a.z += ws[j] * v[j].z;
-          a.w += ws[j] * v[j].w;
-        }
-      }
-      if (r1 - r0 <= kRun) {
-        float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
-        float4 o = *dst;
-        o.x += a.x;
-        o.y += a.y;
-        o.z += a.z;
-        o.w += a.w;
-        *dst = o;
-      } else {
-        *reinterpret_cast<float4*>(y + (size_t)ps[0] * ldy + c) = a;
-      }
-    }
-  }
-}
-
-__global__ __launch_bounds__(256) void combine_partials_kernel(const float* y, int ldy, const int* rrow,
-                                                               const int* rptr, const int* rpair, int nr, float* out,
-                                                               int ldo, int H) {
-  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
-  if (c >= H) return;
-  for (int i = blockIdx.y; i < nr; i += gridDim.y) {
-    const int r0 = rptr[i], r1 = rptr[i + 1];
-    if (r1 - r0 <= kRun) continue;
-    const int runs = (r1 - r0 + kRun - 1) / kRun;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < runs; s0 += 8) {
-      float4 v[8];
+    if (c < H) {
+      for (int t0 = r0 + j; t0 < r1; t0 += 64 * 8) {
+        float4 v[8];
+        float w[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int s = s0 + j < runs ? s0 + j : s0;
-        v[j] = *reinterpret_cast<const float4*>(y + (size_t)rpair[r0 + s * kRun] * ldy + c);
-      }
+        for (int u = 0; u < 8; ++u) {
+          const int t = t0 + 64 * u;
+          const int p = rpair[t < r1 ? t : t0];
+          w[u] = t < r1 ? pw[p] : 0.f;
+          v[u] = *reinterpret_cast<const float4*>(y + (size_t)p * ldy + c);
+        }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (s0 + j < runs) {
-          a.x += v[j].x;
-          a.y += v[j].y;
-          a.z += v[j].z;
-          a.w += v[j].w;
+        for (int u = 0; u < 8; ++u) {
+          if (t0 + 64 * u < r1) {
+            a.x += w[u] * v[u].x;
+            a.y += w[u] * v[u].y;
+            a.z += w[u] * v[u].z;
+            a.w += w[u] * v[u].w;
+          }
         }
       }
     }
-    float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
-    float4 o = *dst;
-    o.x += a.x;
-    o.y += a.y;
-    o.z += a.z;
-    o.w += a.w;
-    *dst = o;
+    red[j][q] = a;
+    __syncthreads();
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) {
+      if (j < s) {
+        const float4 b = red[j + s][q];
+        float4& d = red[j][q];
+        d.x += b.x;
+        d.y += b.y;
+        d.z += b.z;
+        d.w += b.w;
+      }
+      __syncthreads();
+    }
+    if (j == 0 && c < H) {
+      float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+      const float4 t = red[0][q];
+      float4 o = *dst;
+      o.x += t.x;
+      o.y += t.y;
+      o.z += t.z;
+      o.w += t.w;
+      *dst = o;
+    }
+    __syncthreads();  // red is reused by the next row
   }
 }
 
@@ -168,12 +142,9 @@ int run_combine_runs(float* y, int ldy, const float* pw, const int* rrow, const 
   if (nr <= 0) return MOE_OK;
   const bool vec4 = H % 4 == 0 && ldy % 4 == 0 && ldo % 4 == 0 && aligned(y, 16) && aligned(out, 16);
   if (!vec4) return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, st);
-  const int runs = (max_pairs + kRun - 1) / kRun;
-  const dim3 grid((H + 1023) / 1024, nr < 65535 ? nr : 65535, runs < 1 ? 1 : (runs < 1024 ? runs : 1024));
-  hipLaunchKernelGGL(combine_runs_kernel, grid, dim3(256), 0, st, y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H);
-  if (runs > 1)
-    hipLaunchKernelGGL(combine_partials_kernel, dim3(grid.x, grid.y), dim3(256), 0, st, y, ldy, rrow, rptr, rpair, nr,
-                       out, ldo, H);
+  (void)max_pairs;  // the tree takes any number of pairs a row
+  hipLaunchKernelGGL(combine_tree_kernel, dim3((H + 15) / 16, nr < 65535 ? nr : 65535), dim3(256), 0, st, y, ldy, pw,
+                     rrow, rptr, rpair, nr, out, ldo, H);
   return check_launch("weighted combine");
 }
 

@@ -95,13 +95,13 @@ int moe_gguf_dequant(const uint8_t* raw, int qtype, int O, int cols, float* out,
  * The middle of Expert.__call__, moelan/experts.py:256-259 (silu :62-63). */
 int moe_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, void* stream);
 
-/* out[rrow[i]] += sum over q in rptr[i]..rptr[i+1] of pw[p] * y[p], p = rpair[q],
- * summed in that order in runs of 8 pairs (the runs' sums then added in run
- * order) and then added to out: the weighted combine of per-expert outputs,
- * out[rows] += e(x[rows]) * w, moelan/experts.py:648-651, 707-727 and
- * moelan/kernels.py:778-782, 968. y [P, H] (stride ldy) is also scratch: its
- * contents are overwritten. max_pairs bounds the pairs of one row (0: not
- * known; one workgroup then sums a whole row). out stride ldo. */
+/* out[rrow[i]] += sum over q in rptr[i]..rptr[i+1] of pw[p] * y[p], p = rpair[q]:
+ * the weighted combine of per-expert outputs, out[rows] += e(x[rows]) * w,
+ * moelan/experts.py:648-651, 707-727 and moelan/kernels.py:778-782, 968.
+ * Summed in a fixed order (64 strided partial sums, each in list order, added
+ * by a fixed binary tree), so results repeat bit for bit; no atomics. y [P, H]
+ * (stride ldy) is only read. max_pairs (an upper bound of a row's pairs, or 0)
+ * is accepted and not needed. out stride ldo. */
 int moe_combine(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
                 int max_pairs, float* out, int ldo, int H, void* stream);
 
