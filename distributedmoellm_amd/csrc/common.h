@@ -28,6 +28,7 @@ int check_launch(const char* what);
 __host__ __device__ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // Pointers in the global address space: loads through them are global_load_*
 // (counted by vmcnt only), not flat loads, even when the address came from memory.

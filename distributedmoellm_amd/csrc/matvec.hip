@@ -280,6 +280,146 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
   }
 }
 
+// ------------------------------------------------------------------ 24-byte int4 chunks
+//
+// Rows whose 16-byte chunk count is not a power of two leave lanes of every
+// group idle (384-byte rows: 24 chunks, 24 of 32 lanes busy). Cut into
+// 24-byte chunks (48 values) such rows can fill a group (384 bytes: 16
+// chunks, 16 lanes). A chunk is three sub-chunks of 16 values, each inside
+// one scale group (gs a multiple of 16), so each sub-chunk has its own scale.
+struct Q4W24 {
+  static constexpr int XR = 51;
+
+  // xr[m] = x[2m] - x[2m+1]/16, xr[24+m] = x[2m+1]/16 (byte m of the chunk),
+  // xr[48+k] = sum of sub-chunk k's 16 values
+  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {  // one sub-chunk at a time keeps the set-up's registers few
+      float v[16];
+      xs.run<16>(chunk * 48 + 16 * k, v);
+      float sum = 0.f;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const float xe = v[2 * m], xo = v[2 * m + 1];
+        xr[8 * k + m] = xe - xo * 0.0625f;
+        xr[24 + 8 * k + m] = xo * 0.0625f;
+        sum += xe + xo;
+      }
+      xr[48 + k] = sum;
+    }
+  }
+
+  // sum over sub-chunk k (words 2k, 2k+1) of (u - 8) * x
+  __device__ static float sub(const uint32_t (&w)[6], uint32_t xor4, const float* xr, int k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 2 * k; i < 2 * k + 2; ++i) {
+      const uint32_t a = w[i] ^ xor4;
+      const uint32_t lo = opaque(a & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        acc = fmaf(ubyte(lo, b), xr[4 * i + b], acc);
+        acc = fmaf(ubyte(a, b), xr[24 + 4 * i + b], acc);
+      }
+    }
+    return fmaf(-8.0f, xr[48 + k], acc);
+  }
+};
+
+// As mv_fast_body with one 24-byte chunk per lane and one input row: L lanes
+// per row (all busy), two passes of 64/L rows per register buffer, two
+// buffers. Weights are read as three 8-byte words (24-byte offsets are
+// 8-byte aligned when the matrix is).
+template <int L, int G, bool SF16>
+__device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job, const MatRef& M, int ng, int p0,
+                                            int p1, int row_begin) {
+  constexpr int RPP = 64 / L;
+  const int lane = threadIdx.x & 63;
+  const int lg = lane / L, lc = lane % L;
+  const uint32_t woff = (uint32_t)lc * 24u;
+  uint32_t soff[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) soff[k] = (uint32_t)((48 * lc + 16 * k) / sh.gs);
+  const uint32_t omax = (uint32_t)sh.O - 1u, rb = (uint32_t)sh.row_bytes, gpr = (uint32_t)sh.G;
+  const uint8_t* const W = M.w;
+  const void* const S = M.s;
+
+  for (int p = p0; p < p1; ++p) {
+    float xr[Q4W24::XR];
+    {
+      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+      Q4W24::load_x(xs, lc, xr);
+    }
+    uint32_t wb[2][G][6];
+    uint32_t sb[2][G][3];
+    auto issue = [&](auto buf, int grp) {
+      constexpr int B = decltype(buf)::value;
+      const uint32_t obase = (uint32_t)(row_begin + grp * (G * RPP) + lg);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t o = min(obase + (uint32_t)(g * RPP), omax);
+        const uint32_t wrow = __umul24(o, rb), srow = __umul24(o, gpr);
+        const MOE_GLOBAL u32x2* wp = gptr<u32x2>(W + (wrow + woff));
+#pragma unroll
+        for (int h = 0; h < 3; ++h) {
+          const u32x2 v = __builtin_nontemporal_load(wp + h);
+          wb[B][g][2 * h] = v.x;
+          wb[B][g][2 * h + 1] = v.y;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) sb[B][g][k] = sload_bits<SF16>(S, srow + soff[k]);
+      }
+    };
+    auto compute = [&](auto buf, int grp) {
+      constexpr int B = decltype(buf)::value;
+      const int obase = row_begin + grp * (G * RPP) + lg;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) a = fmaf(Q4W24::sub(wb[B][g], M.xor4, xr, k), scale_value<SF16>(sb[B][g][k]), a);
+        a = lane_group_sum<L>(a);
+        const int o = obase + g * RPP;
+        if (lc == L - 1 && o < sh.O) job.y[(size_t)p * job.ldy + o] = a;
+      }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    issue(B0{}, 0);
+    int grp = 0;
+    for (; grp + 2 < ng; grp += 2) {
+      issue(B1{}, grp + 1);
+      compute(B0{}, grp);
+      issue(B0{}, grp + 2);
+      compute(B1{}, grp + 1);
+    }
+    if (grp + 1 < ng) {
+      issue(B1{}, grp + 1);
+      compute(B0{}, grp);
+      compute(B1{}, grp + 1);
+    } else {
+      compute(B0{}, grp);
+    }
+  }
+}
+
+template <int L, int G>
+__global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, int ng) {
+  const int mat = blockIdx.y;
+  int p0 = 0, p1 = job.n;
+  if (job.seg) {
+    p0 = job.seg[mat];
+    p1 = job.seg[mat + 1];
+  }
+  if (p0 >= p1) return;
+  const int wave = threadIdx.x >> 6;
+  const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * ng * G * (64 / L);
+  if (row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
+  const MatRef M = resolve(job, mat);
+  if (M.s_f16) mv_w24_body<L, G, true>(sh, job, M, ng, p0, p1, row_begin);
+  else mv_w24_body<L, G, false>(sh, job, M, ng, p0, p1, row_begin);
+}
+
 // One launch covers every matrix of the call (grid.y); the scale type and the
 // weight alignment are uniform per matrix, so the specialised body is chosen
 // once at the top.
@@ -705,11 +845,43 @@ static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_r
   return false;
 }
 
+// 24-byte chunks for int4 rows whose 16-byte chunks do not fill a lane group
+// but whose 24-byte chunks do (8, 16, 32 or 64 of them); one input row a pair
+static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
+  static const int off = [] {
+    const char* e = getenv("MOEHIP_MV_NO24");  // measurement switch: keep 16-byte chunks
+    return e && e[0] == '1';
+  }();
+  if (off || max_rows != 1 || sh.row_bytes % 24 != 0 || sh.gs % 16 != 0 || !offsets_fit(sh)) return false;
+  const int c16 = sh.row_bytes / 16, c24 = sh.row_bytes / 24;
+  if (sh.row_bytes % 16 == 0 && (c16 & (c16 - 1)) == 0) return false;  // 16-byte chunks fill their groups
+  int L = 0;
+  if (c24 == 8 || c24 == 16 || c24 == 32 || c24 == 64) L = c24;
+  if (L == 0) return false;
+  constexpr int G = 2;  // passes per register buffer (1: 126 VGPRs, 4 waves a SIMD, measured no faster)
+  const int rpp = 64 / L;
+  const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));
+  const int ng_max = job.half_in > 0 ? 32 : 16;
+  int ng = (int)(groups / 2048);
+  ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
+  const int wave_rows = ng * G * rpp;
+  const int waves = (sh.O + wave_rows - 1) / wave_rows;
+  const dim3 grid((waves + 3) / 4, nmat);
+  switch (L) {
+    case 8: hipLaunchKernelGGL((mv_q4w24_kernel<8, G>), grid, dim3(256), 0, st, sh, job, ng); break;
+    case 16: hipLaunchKernelGGL((mv_q4w24_kernel<16, G>), grid, dim3(256), 0, st, sh, job, ng); break;
+    case 32: hipLaunchKernelGGL((mv_q4w24_kernel<32, G>), grid, dim3(256), 0, st, sh, job, ng); break;
+    default: hipLaunchKernelGGL((mv_q4w24_kernel<64, G>), grid, dim3(256), 0, st, sh, job, ng); break;
+  }
+  return true;
+}
+
 int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   if (max_rows <= 0 || nmat <= 0 || sh.O <= 0) return MOE_OK;
   int per, size, vals;
   if (block_geometry(fmt, &per, &size, &vals)) return run_matvec_blocks(fmt, sh, job, nmat, st);  // GGUF
   if (chunked_ok(fmt, sh)) {
+    if (fmt == FMT_Q4 && launch_w24(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec (24-byte chunks)");
     if (fmt == FMT_Q4 && launch_fast<FmtQ4>(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec");
     if (fmt == FMT_Q8 && launch_fast<FmtQ8>(sh, job, nmat, max_rows, st)) return check_launch("int8 mat-vec");
     const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);

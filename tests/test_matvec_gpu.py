@@ -194,3 +194,36 @@ def test_gguf_dequant_bit_exact_on_random_bytes(kernels, qtype):
     assert np.array_equal(np.isfinite(out), ok)
     assert np.array_equal(out[ok], want[ok])
     assert np.array_equal(np.isnan(out), np.isnan(want))
+
+
+# ---------------------------------------------------------------- 24-byte chunks (one input row)
+
+W24_SHAPES = [(200, 384, 32), (2048, 768, 32), (2048, 768, 16), (1000, 768, 48), (2048, 768, 64),
+              (4096, 1536, 32), (96, 3072, 64)]
+
+
+@pytest.mark.parametrize("O,I,gs", W24_SHAPES)
+@pytest.mark.parametrize("offset", [False, True])
+@pytest.mark.parametrize("sdt", [np.float16, np.float32])
+def test_q4_w24_single_row(kernels, O, I, gs, offset, sdt):
+    """Rows whose 16-byte chunks leave lanes idle but whose 24-byte chunks fill
+    8, 16, 32 or 64 lanes (I = 384, 768, 1536, 3072), one input row."""
+    rng = np.random.default_rng(O + I + gs)
+    raw, s = int4_matrix(rng, O, I, gs, sdt)
+    if sdt == np.float32:
+        s = rng.random(s.shape).astype(np.float32) * 1e-3
+    x = rng.standard_normal((1, I)).astype(np.float32)
+    close(kernels.q4_matmul_t(x, raw, s, gs, offset), R.q4_matmul_t(x, raw, s, gs, offset))
+
+
+def test_q4_w24_one_hot_columns_are_exact(kernels):
+    """x = e_c, one row at a time: column c of W bit-exactly, across sub-chunk and group edges."""
+    rng = np.random.default_rng(3)
+    O, I, gs = 256, 768, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    W = R.q4_dequant(raw, s, gs, False)
+    for c in [0, 1, 15, 16, 31, 32, 47, 48, 63, 64, 95, 96, 767]:
+        x = np.zeros((1, I), np.float32)
+        x[0, c] = 1.0
+        y = kernels.q4_matmul_t(x, raw, s, gs, False)
+        assert np.array_equal(y[0], W[:, c]), f"column {c}"
