@@ -584,7 +584,7 @@ def cpu_baseline_prefill(seconds: float = 6.0):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--extras", action="store_true",
