@@ -124,3 +124,16 @@ def test_unaligned_rows_take_the_scalar_kernels(kernels, wire):
     flat = dst.cpu().numpy().reshape(-1)
     got = flat[1 + np.arange(n)[:, None] * (d + 1) + np.arange(d)[None, :]]
     assert np.array_equal(got, back)
+
+
+@pytest.mark.parametrize("wire", ["f32", "f16", "int8"])
+def test_empty_rows(kernels, wire):
+    """No touched rows (a worker with nothing routed to it): empty arrays both ways."""
+    got = W.encode_rows(np.zeros((0, 128), np.float32), wire, "y")
+    assert got["y"].shape == (0, 128)
+    if wire == "int8":
+        assert got["y_scale"].shape == (0, 2)
+    y = torch.zeros((4, 128), device="cuda")
+    got = W.encode_rows(y, wire, "y", rows=np.zeros(0, np.int32))
+    assert got["y"].shape == (0, 128)
+    assert W.decode_rows({k: v.cpu().numpy() for k, v in got.items()}, "y").shape == (0, 128)
