@@ -125,8 +125,8 @@ size_t moe_q4_layer_workspace(int P, int H, int I);
  * given as table[eidx[m]] (eidx NULL: table[m]) with pairs poff[m]..poff[m+1]
  * (input rows prow[p], gate weights pw[p]). Rows touched: rrow[0..nr), whose
  * pairs are rpair[rptr[i]..rptr[i+1]] in ascending order; each row's sum is
- * formed in that order (in runs of 8 pairs, the runs' sums added in run
- * order) and then added to out, as the reference does.
+ * formed in a fixed order (as moe_combine) and then added to out, as the
+ * reference does.
  * max_rows: the largest poff[m+1]-poff[m]. All arrays: device.
  * Replaces moe_q4(x, items, H, I, gs, out), moelan/kernels.py:942-968
  * (_moe_q4 :712-782, float activations). */
