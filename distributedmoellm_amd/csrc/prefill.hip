@@ -146,6 +146,32 @@ __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
   }
 }
 
+// one step of a DPP reduction: the (value, index) of the lane CTRL names, or
+// (sv, si) where that lane is out of the row (the lanes ROWMASK leaves out keep
+// (sv, si) too)
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ void dpp_better(float& v, int& i, float sv, int si) {
+  const float ov = __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, sv), __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false));
+  const int oi = __builtin_amdgcn_update_dpp(si, i, CTRL, ROWMASK, 0xf, false);
+  better(v, i, ov, oi);
+}
+
+// the wave's best (value, index) -- larger value, then lower index -- in every
+// lane: DPP row shifts and broadcasts into lane 63, then read out of it
+__device__ __forceinline__ void wave_best(float& v, int& i) {
+  const float sv = -INFINITY;
+  const int si = 0x7fffffff;
+  dpp_better<0x111, 0xf>(v, i, sv, si);  // row_shr:1
+  dpp_better<0x112, 0xf>(v, i, sv, si);  // row_shr:2
+  dpp_better<0x114, 0xf>(v, i, sv, si);  // row_shr:4
+  dpp_better<0x118, 0xf>(v, i, sv, si);  // row_shr:8
+  dpp_better<0x142, 0xa>(v, i, sv, si);  // row_bcast:15 into rows 1, 3
+  dpp_better<0x143, 0xc>(v, i, sv, si);  // row_bcast:31 into rows 2, 3
+  v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  i = __builtin_amdgcn_readlane(i, 63);
+}
+
 // One wave per token: softmax over E <= 256 logits (f32: x - max, exp, / sum),
 // k picks by repeated arg-max (ties to the lower expert id, as a stable
 // descending sort), then w / sum(w) when normalising.
@@ -190,11 +216,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* logits, int nz,
       const int e = lane + 64 * j;
       if (e < E && !taken[j]) better(bv, bi, v[j], e);
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      better(bv, bi, ov, oi);
-    }
+    wave_best(bv, bi);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (lane + 64 * j == bi) taken[j] = true;
