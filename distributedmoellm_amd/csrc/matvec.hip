@@ -15,6 +15,7 @@
 // A lane computes sum(chunk of weights * chunk of x) * group scale; partial
 // sums of a row are added across its cpr lanes with cross-lane shuffles when
 // cpr is a power of two <= 64, else through LDS.
+#include <atomic>
 #include "common.h"
 #include "formats.h"
 #include "matvec.h"
@@ -197,27 +198,6 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
 
   for (int pb = p0; pb < p1; pb += NR) {
     float xr[NR][CPL][F::XR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      if (pb + r < p1) {
-        const int p = pb + r;
-        const int xrow = job.xrow ? job.xrow[p] : p;
-        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          if (active) F::load_x(xs, lc + c * A, xr[r][c]);
-          else
-#pragma unroll
-            for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c)
-#pragma unroll
-          for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
-      }
-    }
-
     uint4 wb[2][G][CPL];
     uint32_t sb[2][G][CPL];
     // buffers are named by compile-time constants only, so they stay in VGPRs
@@ -259,10 +239,31 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    // steady state with unconditional issues (the compiler's wait counts then
-    // leave one buffer in flight while the other is used), then the last one
-    // or two groups
+    // the first weights go out before the activations are read, so that their
+    // latencies overlap; then the steady state with unconditional issues (the
+    // compiler's wait counts leave one buffer in flight while the other is
+    // used), then the last one or two groups
     issue(B0{}, 0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (pb + r < p1) {
+        const int p = pb + r;
+        const int xrow = job.xrow ? job.xrow[p] : p;
+        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          if (active) F::load_x(xs, lc + c * A, xr[r][c]);
+          else
+#pragma unroll
+            for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+      }
+    }
     int grp = 0;
     for (; grp + 2 < ng; grp += 2) {
       issue(B1{}, grp + 1);
@@ -346,10 +347,6 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
 
   for (int p = p0; p < p1; ++p) {
     float xr[Q4W24::XR];
-    {
-      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
-      Q4W24::load_x(xs, lc, xr);
-    }
     uint32_t wb[2][G][6];
     uint32_t sb[2][G][3];
     auto issue = [&](auto buf, int grp) {
@@ -385,7 +382,11 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    issue(B0{}, 0);
+    issue(B0{}, 0);  // before the activations are read: the latencies overlap
+    {
+      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+      Q4W24::load_x(xs, lc, xr);
+    }
     int grp = 0;
     for (; grp + 2 < ng; grp += 2) {
       issue(B1{}, grp + 1);
@@ -403,8 +404,169 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
   }
 }
 
-template <int L, int G>
-__global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, int ng) {
+// ------------------------------------------------------------------ 24-byte chunks through an LDS ring
+//
+// mv_w24_body holds its prefetched rows in VGPRs: two passes in flight per
+// wave at 158 VGPRs, three waves a SIMD -- about 46 KB in flight per CU, less
+// than HBM needs to stay busy. The ring variant streams a wave's run of rows
+// (contiguous bytes) and their scales with direct-to-LDS loads
+// (global_load_lds_dwordx4: 1 KB a wave per instruction, no VGPRs held) into
+// a ring of NS stages of two passes, NS - 1 stages in flight, and computes
+// from LDS. Waits are explicit: loads return in issue order, so before stage
+// j is read, `s_waitcnt vmcnt(n * D)` (D loads a stage, n stages issued after
+// j) leaves exactly the later stages in flight; stores of y issued in between
+// count too and can only lengthen the wait. The ring is read by ds_read
+// instructions in inline asm that end with their own lgkmcnt wait: the
+// compiler tracks direct-to-LDS loads but cannot tell the ring's stages apart
+// and would wait for every load in flight before any LDS read it sees.
+//
+// Stage layout: the weights of 2 * 64 / L rows (3072 bytes: 64 lanes x 24
+// bytes a pass), then their scales (sst bytes, at most 1024). A matrix takes
+// the ring when its weights and scales are 16-byte aligned and a stage's
+// scales fill whole 16-byte loads; otherwise the wave runs mv_w24_body.
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes a lane into LDS at lds + 16 lane, nontemporal (the `nt` cache
+// policy, as the register path's streaming loads: rows are read once)
+__device__ __forceinline__ void dma16(const void* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 2);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// wait until at most n * D vector-memory operations are outstanding
+template <int D, int NMAX>
+__device__ __forceinline__ void wait_stages(int n) {
+  static_assert(NMAX <= 3 && 3 * D <= 63, "vmcnt is 6 bits");
+  if (n <= 0) wait_vmcnt<0>();
+  else if (n == 1 || NMAX == 1) wait_vmcnt<D>();
+  else if (n == 2 || NMAX == 2) wait_vmcnt<2 * D>();
+  else wait_vmcnt<3 * D>();
+}
+
+// one stage's operands for this lane: the 24-byte chunk of two passes
+// (addresses a0, a1) and the three scales of each (s0.., s1..), then the wait
+template <bool SF16>
+__device__ __forceinline__ void lds_stage24(uint32_t a0, uint32_t a1, const uint32_t (&sa)[2][3], uint32_t (&w)[2][6],
+                                            uint32_t (&sc)[2][3]) {
+  u32x2 v0, v1, v2, v3, v4, v5;
+  if constexpr (SF16) {
+    asm volatile(
+        "ds_read_b64 %0, %12\n\tds_read_b64 %1, %12 offset:8\n\tds_read_b64 %2, %12 offset:16\n\t"
+        "ds_read_b64 %3, %13\n\tds_read_b64 %4, %13 offset:8\n\tds_read_b64 %5, %13 offset:16\n\t"
+        "ds_read_u16 %6, %14\n\tds_read_u16 %7, %15\n\tds_read_u16 %8, %16\n\t"
+        "ds_read_u16 %9, %17\n\tds_read_u16 %10, %18\n\tds_read_u16 %11, %19\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(sc[0][0]), "=&v"(sc[0][1]),
+          "=&v"(sc[0][2]), "=&v"(sc[1][0]), "=&v"(sc[1][1]), "=&v"(sc[1][2])
+        : "v"(a0), "v"(a1), "v"(sa[0][0]), "v"(sa[0][1]), "v"(sa[0][2]), "v"(sa[1][0]), "v"(sa[1][1]), "v"(sa[1][2])
+        : "memory");
+  } else {
+    asm volatile(
+        "ds_read_b64 %0, %12\n\tds_read_b64 %1, %12 offset:8\n\tds_read_b64 %2, %12 offset:16\n\t"
+        "ds_read_b64 %3, %13\n\tds_read_b64 %4, %13 offset:8\n\tds_read_b64 %5, %13 offset:16\n\t"
+        "ds_read_b32 %6, %14\n\tds_read_b32 %7, %15\n\tds_read_b32 %8, %16\n\t"
+        "ds_read_b32 %9, %17\n\tds_read_b32 %10, %18\n\tds_read_b32 %11, %19\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(sc[0][0]), "=&v"(sc[0][1]),
+          "=&v"(sc[0][2]), "=&v"(sc[1][0]), "=&v"(sc[1][1]), "=&v"(sc[1][2])
+        : "v"(a0), "v"(a1), "v"(sa[0][0]), "v"(sa[0][1]), "v"(sa[0][2]), "v"(sa[1][0]), "v"(sa[1][1]), "v"(sa[1][2])
+        : "memory");
+  }
+  const u32x2 v[6] = {v0, v1, v2, v3, v4, v5};
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      w[q][2 * h] = v[3 * q + h].x;
+      w[q][2 * h + 1] = v[3 * q + h].y;
+    }
+}
+
+constexpr int kW24Stage = 2 * 1536;  // weight bytes of a ring stage (two passes)
+
+// the ring's scale bytes a stage for rows of G groups (f16 or f32 scales)
+__host__ __device__ inline uint32_t w24_ring_scales(int L, int G, bool f16) {
+  return (uint32_t)(2 * (64 / L)) * (uint32_t)G * (f16 ? 2u : 4u);
+}
+
+template <int L, int NS, bool SF16>
+__device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job, const MatRef& M, int ng, int p,
+                                            int row_begin, uint8_t* ring, uint32_t stride) {
+  constexpr int RPP = 64 / L, RPS = 2 * RPP;
+  constexpr int kWI = kW24Stage / 1024;  // weight loads a stage
+  constexpr int D = kWI + 1;              // and one for the scales
+  const int lane = threadIdx.x & 63;
+  const int lg = lane / L, lc = lane % L;
+  const uint32_t rb = (uint32_t)sh.row_bytes, sbr = (uint32_t)sh.G * (SF16 ? 2u : 4u);
+  const uint32_t sst = RPS * sbr;
+  const uint32_t wlast = (uint32_t)sh.O * rb - 16u, slast = ((uint32_t)sh.O * sbr - 16u) & ~15u;
+  const uint8_t* const W = M.w;
+  const uint8_t* const S = static_cast<const uint8_t*>(M.s);
+  // this lane's LDS offsets inside a stage
+  const uint32_t ring0 = (uint32_t)(uintptr_t)ring;  // the low 32 bits of a shared address are its LDS offset
+  uint32_t wof[2], sof[2][3];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    wof[q] = (uint32_t)(q * RPP + lg) * rb + 24u * (uint32_t)lc;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      sof[q][k] = (uint32_t)kW24Stage + (uint32_t)(q * RPP + lg) * sbr +
+                  (uint32_t)((48 * lc + 16 * k) / sh.gs) * (SF16 ? 2u : 4u);
+  }
+  const bool s_lane = (uint32_t)lane * 16u < sst;
+  // stage j's rows into ring slot `slot`
+  auto issue = [&](int j, int slot) {
+    uint8_t* st = ring + slot * stride;
+    const uint32_t r0 = (uint32_t)(row_begin + j * RPS);
+    const uint32_t wb = r0 * rb + 16u * (uint32_t)lane;
+#pragma unroll
+    for (int i = 0; i < kWI; ++i) dma16(W + min(wb + 1024u * i, wlast), st + 1024 * i);
+    if (s_lane) dma16(S + min(r0 * sbr + 16u * (uint32_t)lane, slast), st + kW24Stage);
+  };
+  // the first stages go out before the activations are read, so that their
+  // latencies overlap (a wave of fewer stages loads its last one again into
+  // the slots it does not use: a fixed number of loads)
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j) issue(min(j, ng - 1), j);
+  float xr[Q4W24::XR];
+  {
+    const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+    Q4W24::load_x(xs, lc, xr);
+  }
+  for (int j = 0; j < ng; ++j) {
+    if (j + NS - 1 < ng) issue(j + NS - 1, (j + NS - 1) % NS);
+    wait_stages<D, NS - 1>(min(ng - 1 - j, NS - 1));
+    const uint32_t st = ring0 + (uint32_t)(j % NS) * stride;
+    uint32_t sa[2][3];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) sa[q][k] = st + sof[q][k];
+    uint32_t w[2][6], sc[2][3];
+    lds_stage24<SF16>(st + wof[0], st + wof[1], sa, w, sc);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) a = fmaf(Q4W24::sub(w[q], M.xor4, xr, k), scale_value<SF16>(sc[q][k]), a);
+      a = lane_group_sum<L>(a);
+      const int o = row_begin + j * RPS + q * RPP + lg;
+      if (lc == L - 1 && o < sh.O) job.y[(size_t)p * job.ldy + o] = a;
+    }
+  }
+}
+
+// ring_stride > 0: waves stream through LDS rings of NS stages of that many
+// bytes (dynamic LDS, 4 rings a block), ng stages a wave; 0: mv_w24_body, ng
+// groups of G passes a wave
+template <int L, int G, int NS>
+__global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, int ng, int ring_stride) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t w24_ring[];
   const int mat = blockIdx.y;
   int p0 = 0, p1 = job.n;
   if (job.seg) {
@@ -413,11 +575,24 @@ __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, in
   }
   if (p0 >= p1) return;
   const int wave = threadIdx.x >> 6;
-  const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * ng * G * (64 / L);
+  const int wave_rows = ring_stride > 0 ? ng * 2 * (64 / L) : ng * G * (64 / L);
+  const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * wave_rows;
   if (row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
   const MatRef M = resolve(job, mat);
-  if (M.s_f16) mv_w24_body<L, G, true>(sh, job, M, ng, p0, p1, row_begin);
-  else mv_w24_body<L, G, false>(sh, job, M, ng, p0, p1, row_begin);
+  if (ring_stride > 0 && p1 - p0 == 1 && aligned(M.w, 16) && aligned(M.s, 16)) {
+    const uint32_t sst = w24_ring_scales(L, sh.G, M.s_f16 != 0);
+    if (sst % 16 == 0 && (uint32_t)kW24Stage + sst <= (uint32_t)ring_stride &&
+        (uint32_t)sh.O * (uint32_t)sh.G * (M.s_f16 ? 2u : 4u) >= 16u) {
+      uint8_t* ring = w24_ring + (size_t)wave * NS * ring_stride;
+      if (M.s_f16) mv_w24_ring<L, NS, true>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
+      else mv_w24_ring<L, NS, false>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
+      return;
+    }
+  }
+  // the register path covers the wave's rows in groups of G passes
+  const int ngr = (wave_rows + G * (64 / L) - 1) / (G * (64 / L));
+  if (M.s_f16) mv_w24_body<L, G, true>(sh, job, M, ngr, p0, p1, row_begin);
+  else mv_w24_body<L, G, false>(sh, job, M, ngr, p0, p1, row_begin);
 }
 
 // One launch covers every matrix of the call (grid.y); the scale type and the
@@ -845,6 +1020,29 @@ static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_r
   return false;
 }
 
+// Waves of the ring kernel resident on the current device at once for a
+// block LDS size (0 when unknown), cached per device, lane-group width and size.
+template <class K>
+static long w24_ring_slots(K kernel, int L, size_t lds) {
+  struct Entry {
+    std::atomic<long> lds{-1}, slots{0};
+  };
+  static Entry cache[64][4];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  const int li = L == 8 ? 0 : L == 16 ? 1 : L == 32 ? 2 : 3;
+  Entry& e = cache[dev][li];
+  if (e.lds.load() == (long)lds) return e.slots.load();
+  int per_cu = 0, cus = 0;
+  long slots = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) == hipSuccess && per_cu > 0 && cus > 0)
+    slots = 4L * per_cu * cus;
+  e.slots.store(slots);
+  e.lds.store((long)lds);
+  return slots;
+}
+
 // 24-byte chunks for int4 rows whose 16-byte chunks do not fill a lane group
 // but whose 24-byte chunks do (8, 16, 32 or 64 of them); one input row a pair
 static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
@@ -858,22 +1056,54 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
   int L = 0;
   if (c24 == 8 || c24 == 16 || c24 == 32 || c24 == 64) L = c24;
   if (L == 0) return false;
-  constexpr int G = 2;  // passes per register buffer (1: 126 VGPRs, 4 waves a SIMD, measured no faster)
+  constexpr int G = 2;   // passes per register buffer (1: 126 VGPRs, 4 waves a SIMD, measured no faster)
+  constexpr int NS = 3;  // ring stages a wave
+  static const bool ring_off = [] {
+    const char* e = getenv("MOEHIP_MV_RING");  // measurement switch: 0 keeps the register path
+    return e && e[0] == '0';
+  }();
   const int rpp = 64 / L;
-  const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));
-  const int ng_max = job.half_in > 0 ? 32 : 16;
-  int ng = (int)(groups / 2048);
-  ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
-  const int wave_rows = ng * G * rpp;
-  const int waves = (sh.O + wave_rows - 1) / wave_rows;
-  const dim3 grid((waves + 3) / 4, nmat);
+  auto go = [&](auto kernel) {
+    int ng, wave_rows, stride = 0;
+    size_t lds = 0;
+    // the ring's stage: the weights of 2 rpp rows and room for their scales as
+    // f32 (at most 1024 bytes; wider f32 scales take the register path)
+    const uint32_t sf32 = w24_ring_scales(L, sh.G, false);
+    const int ring_stride = kW24Stage + (int)((sf32 > 1024 ? 1024 : sf32) + 15) / 16 * 16;
+    const size_t ring_lds = (size_t)4 * NS * ring_stride;
+    // waves resident at once (LDS-bound), spread evenly over the matrices
+    const long slots = ring_off ? 0 : w24_ring_slots(kernel, L, ring_lds);
+    if (slots > 0) {
+      stride = ring_stride;
+      lds = ring_lds;
+      static const int rounds = [] {
+        const char* e = getenv("MOEHIP_MV_RING_ROUNDS");  // tuning override
+        const int v = e ? atoi(e) : 0;
+        return v >= 1 && v <= 64 ? v : 1;
+      }();
+      const int spm = (sh.O + 2 * rpp - 1) / (2 * rpp);  // stages a matrix
+      long wpm = rounds * slots / nmat;
+      wpm = wpm < 1 ? 1 : (wpm > spm ? spm : wpm);
+      ng = (int)((spm + wpm - 1) / wpm);
+      wave_rows = ng * 2 * rpp;
+    } else {
+      const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));
+      const int ng_max = job.half_in > 0 ? 32 : 16;
+      ng = (int)(groups / 2048);
+      ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
+      wave_rows = ng * G * rpp;
+    }
+    const int waves = (sh.O + wave_rows - 1) / wave_rows;
+    const dim3 grid((waves + 3) / 4, nmat);
+    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, st, sh, job, ng, stride);
+    return true;
+  };
   switch (L) {
-    case 8: hipLaunchKernelGGL((mv_q4w24_kernel<8, G>), grid, dim3(256), 0, st, sh, job, ng); break;
-    case 16: hipLaunchKernelGGL((mv_q4w24_kernel<16, G>), grid, dim3(256), 0, st, sh, job, ng); break;
-    case 32: hipLaunchKernelGGL((mv_q4w24_kernel<32, G>), grid, dim3(256), 0, st, sh, job, ng); break;
-    default: hipLaunchKernelGGL((mv_q4w24_kernel<64, G>), grid, dim3(256), 0, st, sh, job, ng); break;
+    case 8: return go(mv_q4w24_kernel<8, G, NS>);
+    case 16: return go(mv_q4w24_kernel<16, G, NS>);
+    case 32: return go(mv_q4w24_kernel<32, G, NS>);
+    default: return go(mv_q4w24_kernel<64, G, NS>);
   }
-  return true;
 }
 
 int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {

@@ -216,6 +216,31 @@ def test_q4_w24_single_row(kernels, O, I, gs, offset, sdt):
     close(kernels.q4_matmul_t(x, raw, s, gs, offset), R.q4_matmul_t(x, raw, s, gs, offset))
 
 
+@pytest.mark.parametrize("sdt", [np.float16, np.float32])
+@pytest.mark.parametrize("shift", [4, 8])
+def test_q4_w24_unaligned_operands(kernels, sdt, shift):
+    """Weights and scales `shift` bytes past a 16-byte boundary (the LDS ring
+    takes 16-byte aligned operands only; these rows take the register path):
+    the same results as aligned operands."""
+    from distributedmoellm_amd import _lib
+    rng = np.random.default_rng(11 + shift)
+    O, I, gs = 2048, 768, 32
+    raw, s = int4_matrix(rng, O, I, gs, sdt)
+    x = rng.standard_normal((1, I)).astype(np.float32)
+    dev = torch.device("cuda")
+    rb = torch.zeros(raw.nbytes + 16, dtype=torch.uint8, device=dev)
+    rb[shift:shift + raw.nbytes].copy_(torch.from_numpy(raw.reshape(-1)))
+    sb = torch.zeros(s.nbytes + 16, dtype=torch.uint8, device=dev)
+    sb[shift:shift + s.nbytes].copy_(torch.from_numpy(np.ascontiguousarray(s).view(np.uint8).reshape(-1)))
+    xd = torch.from_numpy(x).to(dev)
+    y = torch.empty((1, O), dtype=torch.float32, device=dev)
+    _lib.call("moe_q4_matmul_t", xd.data_ptr(), 1, rb.data_ptr() + shift, sb.data_ptr() + shift,
+              1 if sdt == np.float16 else 0, O, I, gs, 0, y.data_ptr(), kernels.stream_handle())
+    got = y.cpu().numpy()
+    close(got, R.q4_matmul_t(x, raw, s, gs, False))
+    assert np.array_equal(got, kernels.q4_matmul_t(x, raw, s, gs, False))
+
+
 def test_q4_w24_one_hot_columns_are_exact(kernels):
     """x = e_c, one row at a time: column c of W bit-exactly, across sub-chunk and group edges."""
     rng = np.random.default_rng(3)
