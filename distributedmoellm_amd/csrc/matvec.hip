@@ -15,7 +15,9 @@
 // A lane computes sum(chunk of weights * chunk of x) * group scale; partial
 // sums of a row are added across its cpr lanes with cross-lane shuffles when
 // cpr is a power of two <= 64, else through LDS.
-#include <atomic>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include "common.h"
 #include "formats.h"
 #include "matvec.h"
@@ -438,10 +440,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
-// wait until at most n * D vector-memory operations are outstanding
+// wait until at most min(n, NMAX) * D vector-memory operations are outstanding
 template <int D, int NMAX>
 __device__ __forceinline__ void wait_stages(int n) {
-  static_assert(NMAX <= 3 && 3 * D <= 63, "vmcnt is 6 bits");
+  static_assert(NMAX >= 1 && NMAX <= 3 && 3 * D <= 63, "vmcnt is 6 bits");
   if (n <= 0) wait_vmcnt<0>();
   else if (n == 1 || NMAX == 1) wait_vmcnt<D>();
   else if (n == 2 || NMAX == 2) wait_vmcnt<2 * D>();
@@ -503,7 +505,6 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
   const int lane = threadIdx.x & 63;
   const int lg = lane / L, lc = lane % L;
   const uint32_t rb = (uint32_t)sh.row_bytes, sbr = (uint32_t)sh.G * (SF16 ? 2u : 4u);
-  const uint32_t sst = RPS * sbr;
   const uint32_t wlast = (uint32_t)sh.O * rb - 16u, slast = ((uint32_t)sh.O * sbr - 16u) & ~15u;
   const uint8_t* const W = M.w;
   const uint8_t* const S = static_cast<const uint8_t*>(M.s);
@@ -518,24 +519,25 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
       sof[q][k] = (uint32_t)kW24Stage + (uint32_t)(q * RPP + lg) * sbr +
                   (uint32_t)((48 * lc + 16 * k) / sh.gs) * (SF16 ? 2u : 4u);
   }
-  const bool s_lane = (uint32_t)lane * 16u < sst;
-  // stage j's rows into ring slot `slot`
+  // stage j's rows into ring slot `slot`; every lane loads 16 scale bytes
+  // (the stage's scale area is 1024 bytes), so a stage is always D loads
   auto issue = [&](int j, int slot) {
     uint8_t* st = ring + slot * stride;
     const uint32_t r0 = (uint32_t)(row_begin + j * RPS);
     const uint32_t wb = r0 * rb + 16u * (uint32_t)lane;
 #pragma unroll
     for (int i = 0; i < kWI; ++i) dma16(W + min(wb + 1024u * i, wlast), st + 1024 * i);
-    if (s_lane) dma16(S + min(r0 * sbr + 16u * (uint32_t)lane, slast), st + kW24Stage);
+    dma16(S + min(r0 * sbr + 16u * (uint32_t)lane, slast), st + kW24Stage);
   };
-  // the first stages go out before the activations are read, so that their
-  // latencies overlap (a wave of fewer stages loads its last one again into
-  // the slots it does not use: a fixed number of loads)
+  // the input row's index, then the first stages (a wave of fewer stages
+  // loads its last one again into the slots it does not use), then the
+  // activations: the latencies overlap
+  const int xrow = job.xrow ? job.xrow[p] : p;
 #pragma unroll
   for (int j = 0; j < NS - 1; ++j) issue(min(j, ng - 1), j);
   float xr[Q4W24::XR];
   {
-    const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+    const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
     Q4W24::load_x(xs, lc, xr);
   }
   for (int j = 0; j < ng; ++j) {
@@ -1020,27 +1022,37 @@ static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_r
   return false;
 }
 
-// Waves of the ring kernel resident on the current device at once for a
-// block LDS size (0 when unknown), cached per device, lane-group width and size.
-template <class K>
-static long w24_ring_slots(K kernel, int L, size_t lds) {
-  struct Entry {
-    std::atomic<long> lds{-1}, slots{0};
-  };
-  static Entry cache[64][4];
+// Waves of a ring kernel resident on the current device at once for a block
+// size and LDS size (0 when unknown), cached per device, kernel and sizes.
+static long ring_slots(const void* kernel, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int, size_t>, long> cache;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  const int li = L == 8 ? 0 : L == 16 ? 1 : L == 32 ? 2 : 3;
-  Entry& e = cache[dev][li];
-  if (e.lds.load() == (long)lds) return e.slots.load();
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const auto key = std::make_tuple(dev, kernel, threads, lds);
+  {
+    std::lock_guard<std::mutex> g(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
   int per_cu = 0, cus = 0;
   long slots = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) == hipSuccess && per_cu > 0 && cus > 0)
-    slots = 4L * per_cu * cus;
-  e.slots.store(slots);
-  e.lds.store((long)lds);
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) == hipSuccess && per_cu > 0 &&
+      cus > 0)
+    slots = (long)per_cu * (threads / 64) * cus;
+  std::lock_guard<std::mutex> g(mu);
+  cache[key] = slots;
   return slots;
+}
+
+// MOEHIP_MV_RING=0 keeps the register paths (a measurement switch)
+static bool ring_disabled() {
+  static const bool off = [] {
+    const char* e = getenv("MOEHIP_MV_RING");
+    return e && e[0] == '0';
+  }();
+  return off;
 }
 
 // 24-byte chunks for int4 rows whose 16-byte chunks do not fill a lane group
@@ -1058,21 +1070,17 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
   if (L == 0) return false;
   constexpr int G = 2;   // passes per register buffer (1: 126 VGPRs, 4 waves a SIMD, measured no faster)
   constexpr int NS = 3;  // ring stages a wave
-  static const bool ring_off = [] {
-    const char* e = getenv("MOEHIP_MV_RING");  // measurement switch: 0 keeps the register path
-    return e && e[0] == '0';
-  }();
+  const bool ring_off = ring_disabled();
   const int rpp = 64 / L;
   auto go = [&](auto kernel) {
     int ng, wave_rows, stride = 0;
     size_t lds = 0;
-    // the ring's stage: the weights of 2 rpp rows and room for their scales as
-    // f32 (at most 1024 bytes; wider f32 scales take the register path)
-    const uint32_t sf32 = w24_ring_scales(L, sh.G, false);
-    const int ring_stride = kW24Stage + (int)((sf32 > 1024 ? 1024 : sf32) + 15) / 16 * 16;
+    // the ring's stage: the weights of 2 rpp rows and a 1024-byte scale area
+    // (wider scale rows take the register path)
+    const int ring_stride = kW24Stage + 1024;
     const size_t ring_lds = (size_t)4 * NS * ring_stride;
     // waves resident at once (LDS-bound), spread evenly over the matrices
-    const long slots = ring_off ? 0 : w24_ring_slots(kernel, L, ring_lds);
+    const long slots = ring_off ? 0 : ring_slots(reinterpret_cast<const void*>(kernel), 256, ring_lds);
     if (slots > 0) {
       stride = ring_stride;
       lds = ring_lds;
