@@ -688,7 +688,7 @@ def main() -> int:
                      "kernel": k["name"], "avg_launch_us": round(k["avg_us"], 2),
                      "bytes_per_launch": k["bytes_per_launch"],
                      "gate_up": {"us": round(k["gate_up_us"], 2), "gbs": round(k["gate_up_gbs"], 1)},
-                     "down": {"kernel": "mv_q4w24_kernel<16, 2> (the down launch: 384 experts x [2048 x 768])",
+                     "down": {"kernel": "mv_q4w24_kernel<16, 2, 3> (the down launch: 384 experts x [2048 x 768], rows through an LDS ring)",
                               "us": round(k["down_us"], 2), "gbs": round(k["down_gbs"], 1),
                               "bytes_per_launch": k["down_bytes"],
                               "frac": round(k["down_gbs"] / HBM_PEAK_GBS, 4)}},

@@ -519,15 +519,18 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
       sof[q][k] = (uint32_t)kW24Stage + (uint32_t)(q * RPP + lg) * sbr +
                   (uint32_t)((48 * lc + 16 * k) / sh.gs) * (SF16 ? 2u : 4u);
   }
-  // stage j's rows into ring slot `slot`; every lane loads 16 scale bytes
-  // (the stage's scale area is 1024 bytes), so a stage is always D loads
+  // stage j's rows into ring slot `slot`. Every lane loads 16 scale bytes,
+  // so a stage is always D loads (the stage's scale area is 1024 bytes):
+  // lanes past the stage's scales read its first 16 again (the cache line
+  // lane 0 reads, so no extra traffic) into the unused part of the area.
+  const uint32_t slane = (uint32_t)lane * 16u < RPS * sbr ? 16u * (uint32_t)lane : 0u;
   auto issue = [&](int j, int slot) {
     uint8_t* st = ring + slot * stride;
     const uint32_t r0 = (uint32_t)(row_begin + j * RPS);
     const uint32_t wb = r0 * rb + 16u * (uint32_t)lane;
 #pragma unroll
     for (int i = 0; i < kWI; ++i) dma16(W + min(wb + 1024u * i, wlast), st + 1024 * i);
-    dma16(S + min(r0 * sbr + 16u * (uint32_t)lane, slast), st + kW24Stage);
+    dma16(S + min(r0 * sbr + slane, slast), st + kW24Stage);
   };
   // the input row's index, then the first stages (a wave of fewer stages
   // loads its last one again into the slots it does not use), then the
