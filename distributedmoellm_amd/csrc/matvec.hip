@@ -567,7 +567,7 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
 }
 
 // ring_stride > 0: waves stream through LDS rings of NS stages of that many
-// bytes (dynamic LDS, 4 rings a block), ng stages a wave; 0: mv_w24_body, ng
+// bytes (dynamic LDS, one ring a wave), ng stages a wave; 0: mv_w24_body, ng
 // groups of G passes a wave
 template <int L, int G, int NS>
 __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, int ng, int ring_stride) {
