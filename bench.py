@@ -181,8 +181,9 @@ def decode384(args, L, per_layer=False):
     # launch runs mv_q4w24_kernel (768-value rows in 24-byte chunks)
     gu_s, dn_s = gu_ms.mean() / 1e3, dn_ms.mean() / 1e3
     res = dict(ms_per_step=ms, value=step_bytes / (ms / 1e3) / 1e9, step_bytes=step_bytes,
-               kernel=dict(name="mv_fast_kernel<FmtQ4, 64, 1, 1> (int4 decode mat-vec, the gate|up launch of "
-                                "moe_q4_experts_matvec: 384 experts x [1536 x 2048])",
+               kernel=dict(name="mv_fast_kernel<FmtQ4D, 64, 1, 1> (int4 decode mat-vec, integer dot8 on "
+                                "activation limbs; the gate|up launch of moe_q4_experts_matvec: 384 experts x "
+                                "[1536 x 2048])",
                            launches=args.steps, avg_us=gu_s * 1e6, bytes_per_launch=gu_bytes,
                            achieved_gbs=gu_bytes / gu_s / 1e9,
                            gate_up_us=float(gu_ms.mean() * 1e3), down_us=float(dn_ms.mean() * 1e3),
@@ -676,7 +677,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4xf32",
+        "dtype": "int4 x f32 (gate|up: i4 dot8 on 23-bit fixed-point activation limbs, i32 accumulate; "
+                 "down: f32 FMA)",
         "data": "synthetic (seeded uniform nibbles, |N(0,0.02)|/8 f16 scales, N(0,1) activations)",
         "config": {"workload": "int4 expert decode mat-vec: one token's 384 routed-expert evaluations "
                                "(48 layers x top-8) per fused call, Qwen3-30B-A3B expert shape H=2048 I=768, "

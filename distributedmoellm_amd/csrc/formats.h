@@ -111,6 +111,87 @@ struct FmtQ4 {
   }
 };
 
+// ------------------------------------------------------------------ Q4, integer dot
+// The same 32-value chunk as FmtQ4, multiplied with v_dot8c_i32_i4 (8 signed
+// nibbles x 8 signed nibbles, exact) instead of 32 converts and 32 FMAs.
+//  * Activations: the chunk's 32 values as exact fixed point x_int =
+//    rint(x * 2^S), |x_int| <= 2^22, S from the chunk's largest |x|. Each is
+//    the sum of six balanced 4-bit digits d_k * 16^k, d_k in [-8, 7]: the
+//    hex digits of x_int + 0x888888, minus 8. Limb word 6 j + k holds digit
+//    k of the 8 values of weight word j, value i in nibble i, as two's
+//    complement. xr[24] = 2^-S (NaN when the chunk holds a non-finite value).
+//  * Weights: u ^ 8 is the signed nibble u - 8 (u = stored ^ xor4).
+//  * Dot: acc_k = sum over the 4 words of dot8(w, limb k), exact; the chunk's
+//    sum (u - 8) * x_int = sum acc_k 16^k, formed as two exact 3-limb
+//    integers joined by one rounding, then scaled by 2^-S.
+// Each product term is off by at most |u - 8| * 2^-(S+1) <= 8 * 2^-23 of the
+// chunk's largest |x|, and a one-hot x is exact.
+struct FmtQ4D {
+  static constexpr int VALS = 32;
+  static constexpr int XR = 25;
+  static constexpr int BYTES = 16;
+
+  // limb words of 8 biased values xb (24 bits each): six words, digit k of
+  // value i in nibble i of word k, XOR 8 per nibble (two's complement digit)
+  __device__ static void limbs8(const uint32_t* xb, uint32_t* out) {
+    uint32_t E[4], O[4];  // byte n of E[p]: digit 2n of values 2p (low nibble) and 2p+1; O: digit 2n+1
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      E[p] = (xb[2 * p] & 0x0F0F0F0Fu) | ((xb[2 * p + 1] << 4) & 0xF0F0F0F0u);
+      O[p] = ((xb[2 * p] >> 4) & 0x0F0F0F0Fu) | (xb[2 * p + 1] & 0xF0F0F0F0u);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t* src = h ? O : E;
+      // byte gathers: perm(hi, lo, sel) picks bytes 0-3 of lo, 4-7 of hi
+      const uint32_t p01 = __builtin_amdgcn_perm(src[1], src[0], 0x05010400u);  // E0.b0 E2.b0 E0.b1 E2.b1
+      const uint32_t p45 = __builtin_amdgcn_perm(src[3], src[2], 0x05010400u);
+      const uint32_t q01 = __builtin_amdgcn_perm(src[1], src[0], 0x06020602u);  // E0.b2 E2.b2
+      const uint32_t q45 = __builtin_amdgcn_perm(src[3], src[2], 0x06020602u);
+      out[h + 0] = __builtin_amdgcn_perm(p45, p01, 0x05040100u) ^ 0x88888888u;
+      out[h + 2] = __builtin_amdgcn_perm(p45, p01, 0x07060302u) ^ 0x88888888u;
+      out[h + 4] = __builtin_amdgcn_perm(q45, q01, 0x05040100u) ^ 0x88888888u;
+    }
+  }
+
+  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
+    float v[32];
+    xs.run<32>(chunk * 32, v);
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+    const int S = 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0);
+    uint32_t xb[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xb[i] = (uint32_t)((int)__builtin_rintf(__builtin_ldexpf(v[i], S)) + 0x888888);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w[6];
+      limbs8(xb + 8 * j, w);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) xr[6 * j + k] = __builtin_bit_cast(float, w[k]);
+    }
+    xr[24] = __builtin_ldexpf(1.0f, -S) + (m - m);  // m - m: NaN for a non-finite chunk
+  }
+
+  // sum over the chunk of (u - 8) * x, u the unsigned nibble
+  __device__ static float dot(const uint4 w, uint32_t xor4, const float* xr) {
+    const uint32_t flip = xor4 ^ 0x88888888u;
+    const uint32_t s[4] = {w.x ^ flip, w.y ^ flip, w.z ^ flip, w.w ^ flip};
+    int acc[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      acc[k] = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[k] = __builtin_amdgcn_sdot8((int)s[j], (int)__builtin_bit_cast(uint32_t, xr[6 * j + k]), acc[k], false);
+    }
+    const int lo = acc[0] + 16 * acc[1] + 256 * acc[2];
+    const int hi = acc[3] + 16 * acc[4] + 256 * acc[5];
+    return fmaf((float)hi, 4096.0f, (float)lo) * xr[24];
+  }
+};
+
 // ------------------------------------------------------------------ Q8
 struct FmtQ8 {
   static constexpr int VALS = 16;

@@ -1123,7 +1123,14 @@ int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_r
   if (block_geometry(fmt, &per, &size, &vals)) return run_matvec_blocks(fmt, sh, job, nmat, st);  // GGUF
   if (chunked_ok(fmt, sh)) {
     if (fmt == FMT_Q4 && launch_w24(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec (24-byte chunks)");
-    if (fmt == FMT_Q4 && launch_fast<FmtQ4>(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec");
+    if (fmt == FMT_Q4) {
+      static const bool float_dot = [] {
+        const char* e = getenv("MOEHIP_MV_FLOATDOT");  // measurement switch: 1 keeps the float dot
+        return e && e[0] == '1';
+      }();
+      if (float_dot ? launch_fast<FmtQ4>(sh, job, nmat, max_rows, st) : launch_fast<FmtQ4D>(sh, job, nmat, max_rows, st))
+        return check_launch("int4 mat-vec");
+    }
     if (fmt == FMT_Q8 && launch_fast<FmtQ8>(sh, job, nmat, max_rows, st)) return check_launch("int8 mat-vec");
     const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
     const size_t lds = sh.pow2 ? 0 : (size_t)4 * nr * sh.rpp * (sh.cpr + 1) * sizeof(float);

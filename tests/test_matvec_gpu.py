@@ -74,6 +74,35 @@ def test_q4_one_hot_columns_are_exact(kernels, O, I, gs):
         assert np.array_equal(y[i], W[:, c]), f"column {c}"
 
 
+@pytest.mark.parametrize("spread", [0.0, 3.0, 6.0])
+def test_q4_activation_dynamic_range(kernels, spread):
+    """The 32-value chunks are multiplied as exact fixed point scaled from each
+    chunk's largest |x| (integer dot8 on 4-bit limbs): values spread over
+    `spread` decades inside a chunk, all-zero chunks, and overall scales of
+    1e20 and 1e-20 stay within 1e-5 of the float64 product (four input rows)."""
+    rng = np.random.default_rng(int(spread * 10) + 5)
+    O, I, gs = 1536, 2048, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    x = rng.standard_normal((4, I)) * 10.0 ** rng.uniform(-spread, 0, (4, I))
+    x[1, 64:128] = 0.0
+    x[2] *= 1e20
+    x[3] *= 1e-20
+    x = x.astype(np.float32)
+    close(kernels.q4_matmul_t(x, raw, s, gs, False), R.q4_matmul_t(x, raw, s, gs, False))
+
+
+def test_q4_non_finite_activation_is_not_hidden(kernels):
+    """An inf in the input row makes every output of the row non-finite, as in
+    the float product (where inf * 0 and inf - inf give NaN)."""
+    rng = np.random.default_rng(8)
+    O, I, gs = 256, 2048, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    x = rng.standard_normal((1, I)).astype(np.float32)
+    x[0, 100] = np.inf
+    y = kernels.q4_matmul_t(x, raw, s, gs, False)
+    assert not np.isfinite(y).any()
+
+
 def test_q4_generic_shapes(kernels):
     """Group sizes that split a 32-column chunk and widths not divisible by 32 take the generic kernel."""
     rng = np.random.default_rng(3)
