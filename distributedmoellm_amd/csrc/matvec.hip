@@ -329,11 +329,57 @@ struct Q4W24 {
   }
 };
 
+// The integer dot for the same chunks (as FmtQ4D): each 16-value sub-chunk is
+// exact fixed point from its own largest |x|, six 4-bit limb words per weight
+// word (limb word 12 k + 6 h + l: digit l of word 2 k + h), xr[36 + k] its
+// 2^-S. sub() returns the same sum as Q4W24::sub.
+struct Q4W24D {
+  static constexpr int XR = 39;
+
+  __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      float v[16];
+      xs.run<16>(chunk * 48 + 16 * k, v);
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+      const int S = 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0);
+      uint32_t xb[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xb[i] = (uint32_t)((int)__builtin_rintf(__builtin_ldexpf(v[i], S)) + 0x888888);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t w[6];
+        FmtQ4D::limbs8(xb + 8 * h, w);
+#pragma unroll
+        for (int l = 0; l < 6; ++l) xr[12 * k + 6 * h + l] = __builtin_bit_cast(float, w[l]);
+      }
+      xr[36 + k] = __builtin_ldexpf(1.0f, -S) + (m - m);  // m - m: NaN for a non-finite sub-chunk
+    }
+  }
+
+  // sum over sub-chunk k (words 2k, 2k+1) of (u - 8) * x
+  __device__ static float sub(const uint32_t (&w)[6], uint32_t xor4, const float* xr, int k) {
+    const uint32_t flip = xor4 ^ 0x88888888u;
+    const uint32_t s0 = w[2 * k] ^ flip, s1 = w[2 * k + 1] ^ flip;
+    int acc[6];
+#pragma unroll
+    for (int l = 0; l < 6; ++l) {
+      acc[l] = __builtin_amdgcn_sdot8((int)s0, (int)__builtin_bit_cast(uint32_t, xr[12 * k + l]), 0, false);
+      acc[l] = __builtin_amdgcn_sdot8((int)s1, (int)__builtin_bit_cast(uint32_t, xr[12 * k + 6 + l]), acc[l], false);
+    }
+    const int lo = acc[0] + 16 * acc[1] + 256 * acc[2];
+    const int hi = acc[3] + 16 * acc[4] + 256 * acc[5];
+    return fmaf((float)hi, 4096.0f, (float)lo) * xr[36 + k];
+  }
+};
+
 // As mv_fast_body with one 24-byte chunk per lane and one input row: L lanes
 // per row (all busy), two passes of 64/L rows per register buffer, two
 // buffers. Weights are read as three 8-byte words (24-byte offsets are
 // 8-byte aligned when the matrix is).
-template <int L, int G, bool SF16>
+template <class F, int L, int G, bool SF16>
 __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job, const MatRef& M, int ng, int p0,
                                             int p1, int row_begin) {
   constexpr int RPP = 64 / L;
@@ -348,7 +394,7 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
   const void* const S = M.s;
 
   for (int p = p0; p < p1; ++p) {
-    float xr[Q4W24::XR];
+    float xr[F::XR];
     uint32_t wb[2][G][6];
     uint32_t sb[2][G][3];
     auto issue = [&](auto buf, int grp) {
@@ -376,7 +422,7 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
       for (int g = 0; g < G; ++g) {
         float a = 0.f;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) a = fmaf(Q4W24::sub(wb[B][g], M.xor4, xr, k), scale_value<SF16>(sb[B][g][k]), a);
+        for (int k = 0; k < 3; ++k) a = fmaf(F::sub(wb[B][g], M.xor4, xr, k), scale_value<SF16>(sb[B][g][k]), a);
         a = lane_group_sum<L>(a);
         const int o = obase + g * RPP;
         if (lc == L - 1 && o < sh.O) job.y[(size_t)p * job.ldy + o] = a;
@@ -387,7 +433,7 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
     issue(B0{}, 0);  // before the activations are read: the latencies overlap
     {
       const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
-      Q4W24::load_x(xs, lc, xr);
+      F::load_x(xs, lc, xr);
     }
     int grp = 0;
     for (; grp + 2 < ng; grp += 2) {
@@ -496,7 +542,7 @@ __host__ __device__ inline uint32_t w24_ring_scales(int L, int G, bool f16) {
   return (uint32_t)(2 * (64 / L)) * (uint32_t)G * (f16 ? 2u : 4u);
 }
 
-template <int L, int NS, bool SF16>
+template <class F, int L, int NS, bool SF16>
 __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job, const MatRef& M, int ng, int p,
                                             int row_begin, uint8_t* ring, uint32_t stride) {
   constexpr int RPP = 64 / L, RPS = 2 * RPP;
@@ -538,10 +584,10 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
   const int xrow = job.xrow ? job.xrow[p] : p;
 #pragma unroll
   for (int j = 0; j < NS - 1; ++j) issue(min(j, ng - 1), j);
-  float xr[Q4W24::XR];
+  float xr[F::XR];
   {
     const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
-    Q4W24::load_x(xs, lc, xr);
+    F::load_x(xs, lc, xr);
   }
   for (int j = 0; j < ng; ++j) {
     if (j + NS - 1 < ng) issue(j + NS - 1, (j + NS - 1) % NS);
@@ -558,7 +604,7 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
     for (int q = 0; q < 2; ++q) {
       float a = 0.f;
 #pragma unroll
-      for (int k = 0; k < 3; ++k) a = fmaf(Q4W24::sub(w[q], M.xor4, xr, k), scale_value<SF16>(sc[q][k]), a);
+      for (int k = 0; k < 3; ++k) a = fmaf(F::sub(w[q], M.xor4, xr, k), scale_value<SF16>(sc[q][k]), a);
       a = lane_group_sum<L>(a);
       const int o = row_begin + j * RPS + q * RPP + lg;
       if (lc == L - 1 && o < sh.O) job.y[(size_t)p * job.ldy + o] = a;
@@ -569,7 +615,7 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
 // ring_stride > 0: waves stream through LDS rings of NS stages of that many
 // bytes (dynamic LDS, one ring a wave), ng stages a wave; 0: mv_w24_body, ng
 // groups of G passes a wave
-template <int L, int G, int NS>
+template <class F, int L, int G, int NS>
 __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, int ng, int ring_stride) {
   extern __shared__ __attribute__((aligned(16))) uint8_t w24_ring[];
   const int mat = blockIdx.y;
@@ -589,15 +635,15 @@ __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, in
     if (sst % 16 == 0 && (uint32_t)kW24Stage + sst <= (uint32_t)ring_stride &&
         (uint32_t)sh.O * (uint32_t)sh.G * (M.s_f16 ? 2u : 4u) >= 16u) {
       uint8_t* ring = w24_ring + (size_t)wave * NS * ring_stride;
-      if (M.s_f16) mv_w24_ring<L, NS, true>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
-      else mv_w24_ring<L, NS, false>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
+      if (M.s_f16) mv_w24_ring<F, L, NS, true>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
+      else mv_w24_ring<F, L, NS, false>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
       return;
     }
   }
   // the register path covers the wave's rows in groups of G passes
   const int ngr = (wave_rows + G * (64 / L) - 1) / (G * (64 / L));
-  if (M.s_f16) mv_w24_body<L, G, true>(sh, job, M, ngr, p0, p1, row_begin);
-  else mv_w24_body<L, G, false>(sh, job, M, ngr, p0, p1, row_begin);
+  if (M.s_f16) mv_w24_body<F, L, G, true>(sh, job, M, ngr, p0, p1, row_begin);
+  else mv_w24_body<F, L, G, false>(sh, job, M, ngr, p0, p1, row_begin);
 }
 
 // One launch covers every matrix of the call (grid.y); the scale type and the
@@ -1049,6 +1095,16 @@ static long ring_slots(const void* kernel, int threads, size_t lds) {
   return slots;
 }
 
+// MOEHIP_MV_FLOATDOT=1 keeps the int4 float dot (FmtQ4, Q4W24) in place of
+// the integer dot (FmtQ4D, Q4W24D): a measurement switch
+static bool float_dot() {
+  static const bool on = [] {
+    const char* e = getenv("MOEHIP_MV_FLOATDOT");
+    return e && e[0] == '1';
+  }();
+  return on;
+}
+
 // MOEHIP_MV_RING=0 keeps the register paths (a measurement switch)
 static bool ring_disabled() {
   static const bool off = [] {
@@ -1109,11 +1165,19 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
     hipLaunchKernelGGL(kernel, grid, dim3(256), lds, st, sh, job, ng, stride);
     return true;
   };
+  if (float_dot()) {
+    switch (L) {
+      case 8: return go(mv_q4w24_kernel<Q4W24, 8, G, NS>);
+      case 16: return go(mv_q4w24_kernel<Q4W24, 16, G, NS>);
+      case 32: return go(mv_q4w24_kernel<Q4W24, 32, G, NS>);
+      default: return go(mv_q4w24_kernel<Q4W24, 64, G, NS>);
+    }
+  }
   switch (L) {
-    case 8: return go(mv_q4w24_kernel<8, G, NS>);
-    case 16: return go(mv_q4w24_kernel<16, G, NS>);
-    case 32: return go(mv_q4w24_kernel<32, G, NS>);
-    default: return go(mv_q4w24_kernel<64, G, NS>);
+    case 8: return go(mv_q4w24_kernel<Q4W24D, 8, G, NS>);
+    case 16: return go(mv_q4w24_kernel<Q4W24D, 16, G, NS>);
+    case 32: return go(mv_q4w24_kernel<Q4W24D, 32, G, NS>);
+    default: return go(mv_q4w24_kernel<Q4W24D, 64, G, NS>);
   }
 }
 
@@ -1123,14 +1187,9 @@ int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_r
   if (block_geometry(fmt, &per, &size, &vals)) return run_matvec_blocks(fmt, sh, job, nmat, st);  // GGUF
   if (chunked_ok(fmt, sh)) {
     if (fmt == FMT_Q4 && launch_w24(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec (24-byte chunks)");
-    if (fmt == FMT_Q4) {
-      static const bool float_dot = [] {
-        const char* e = getenv("MOEHIP_MV_FLOATDOT");  // measurement switch: 1 keeps the float dot
-        return e && e[0] == '1';
-      }();
-      if (float_dot ? launch_fast<FmtQ4>(sh, job, nmat, max_rows, st) : launch_fast<FmtQ4D>(sh, job, nmat, max_rows, st))
-        return check_launch("int4 mat-vec");
-    }
+    if (fmt == FMT_Q4 &&
+        (float_dot() ? launch_fast<FmtQ4>(sh, job, nmat, max_rows, st) : launch_fast<FmtQ4D>(sh, job, nmat, max_rows, st)))
+      return check_launch("int4 mat-vec");
     if (fmt == FMT_Q8 && launch_fast<FmtQ8>(sh, job, nmat, max_rows, st)) return check_launch("int8 mat-vec");
     const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
     const size_t lds = sh.pow2 ? 0 : (size_t)4 * nr * sh.rpp * (sh.cpr + 1) * sizeof(float);

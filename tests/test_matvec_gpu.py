@@ -270,6 +270,29 @@ def test_q4_w24_unaligned_operands(kernels, sdt, shift):
     assert np.array_equal(got, kernels.q4_matmul_t(x, raw, s, gs, False))
 
 
+@pytest.mark.parametrize("scale", [1.0, 1e20, 1e-20])
+def test_q4_w24_activation_dynamic_range(kernels, scale):
+    """768-value rows (24-byte chunks, integer dot per 16-value sub-chunk):
+    values spread over 6 decades, all-zero sub-chunks and overall scales of
+    1e20 / 1e-20 stay within 1e-5 of the float64 product."""
+    rng = np.random.default_rng(21)
+    O, I, gs = 2048, 768, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    x = rng.standard_normal((1, I)) * 10.0 ** rng.uniform(-6, 0, (1, I)) * scale
+    x[0, 16:48] = 0.0
+    x = x.astype(np.float32)
+    close(kernels.q4_matmul_t(x, raw, s, gs, False), R.q4_matmul_t(x, raw, s, gs, False))
+
+
+def test_q4_w24_non_finite_activation_is_not_hidden(kernels):
+    rng = np.random.default_rng(22)
+    O, I, gs = 512, 768, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    x = rng.standard_normal((1, I)).astype(np.float32)
+    x[0, 700] = -np.inf
+    assert not np.isfinite(kernels.q4_matmul_t(x, raw, s, gs, False)).any()
+
+
 def test_q4_w24_one_hot_columns_are_exact(kernels):
     """x = e_c, one row at a time: column c of W bit-exactly, across sub-chunk and group edges."""
     rng = np.random.default_rng(3)
