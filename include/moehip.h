@@ -59,7 +59,15 @@ int moe_version(void);
 
 /* y[n, O] = x[n, I] @ W.T for colibri int4 weights, f32 accumulate.
  * Replaces q4_matmul_t(x, raw, s, gs, offset), moelan/kernels.py:1018-1027
- * (kernels _q4 :85-106 and _q4_rows :108-131). x, raw, s, y: device. */
+ * (kernels _q4 :85-106 and _q4_rows :108-131). x, raw, s, y: device.
+ * Numerics (this call, moe_q4_experts_matvec and moe_q4_layer): on the
+ * chunked kernels (rows cut into 16- or 24-byte chunks, which covers the
+ * usual expert shapes) each run of 32 (or 16) activations is taken as exact
+ * fixed point rint(x * 2^S), S set by the run's largest |x|, and multiplied
+ * with the nibbles exactly (integer dot products), then scaled by the group
+ * scale in f32. Each product term is off by at most 8 * 2^-23 of that
+ * largest |x|; a non-finite x makes the outputs that use it non-finite.
+ * Other shapes multiply in f32. */
 int moe_q4_matmul_t(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs,
                     int offset, float* y, void* stream);
 
