@@ -131,6 +131,14 @@ struct FmtQ4D {
   static constexpr int XR = 25;
   static constexpr int BYTES = 16;
 
+  // rint(v * 2^S) + 0x888888 as 24 bits. The clamp to +-2^22 only acts on
+  // non-finite values (finite ones are within it by the choice of S) and
+  // keeps the conversion defined; NaN clamps to -2^22.
+  __device__ static uint32_t fixed_biased(float v, int S) {
+    const float t = fminf(fmaxf(__builtin_rintf(__builtin_ldexpf(v, S)), -4194304.0f), 4194304.0f);
+    return (uint32_t)((int)t + 0x888888);
+  }
+
   // limb words of 8 biased values xb (24 bits each): six words, digit k of
   // value i in nibble i of word k, XOR 8 per nibble (two's complement digit)
   __device__ static void limbs8(const uint32_t* xb, uint32_t* out) {
@@ -143,10 +151,12 @@ struct FmtQ4D {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t* src = h ? O : E;
-      // byte gathers: perm(hi, lo, sel) picks bytes 0-3 of lo, 4-7 of hi
-      const uint32_t p01 = __builtin_amdgcn_perm(src[1], src[0], 0x05010400u);  // E0.b0 E2.b0 E0.b1 E2.b1
+      // byte gathers: perm(hi, lo, sel) picks bytes 0-3 of lo, 4-7 of hi.
+      // p01 = [src0.b0, src1.b0, src0.b1, src1.b1], p45 the same of src2, src3;
+      // q01 = [src0.b2, src1.b2, ...]; digit word n takes byte n of each pair
+      const uint32_t p01 = __builtin_amdgcn_perm(src[1], src[0], 0x05010400u);
       const uint32_t p45 = __builtin_amdgcn_perm(src[3], src[2], 0x05010400u);
-      const uint32_t q01 = __builtin_amdgcn_perm(src[1], src[0], 0x06020602u);  // E0.b2 E2.b2
+      const uint32_t q01 = __builtin_amdgcn_perm(src[1], src[0], 0x06020602u);
       const uint32_t q45 = __builtin_amdgcn_perm(src[3], src[2], 0x06020602u);
       out[h + 0] = __builtin_amdgcn_perm(p45, p01, 0x05040100u) ^ 0x88888888u;
       out[h + 2] = __builtin_amdgcn_perm(p45, p01, 0x07060302u) ^ 0x88888888u;
@@ -163,7 +173,7 @@ struct FmtQ4D {
     const int S = 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0);
     uint32_t xb[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) xb[i] = (uint32_t)((int)__builtin_rintf(__builtin_ldexpf(v[i], S)) + 0x888888);
+    for (int i = 0; i < 32; ++i) xb[i] = fixed_biased(v[i], S);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t w[6];

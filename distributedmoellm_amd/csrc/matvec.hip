@@ -347,7 +347,7 @@ struct Q4W24D {
       const int S = 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0);
       uint32_t xb[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) xb[i] = (uint32_t)((int)__builtin_rintf(__builtin_ldexpf(v[i], S)) + 0x888888);
+      for (int i = 0; i < 16; ++i) xb[i] = FmtQ4D::fixed_biased(v[i], S);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         uint32_t w[6];
