@@ -113,6 +113,28 @@ def test_qwen3_30b_layer_decode(kernels, rows_per_token, k):
     close(out, R.moe_q4(x, oitems, np.zeros(x.shape)))
 
 
+def test_decode_step_384_experts_full_shape(kernels):
+    """The decode benchmark's workload at full size: one token's 384 expert
+    evaluations (48 layers x top-8) in one layer call at the Qwen3-30B-A3B
+    expert shape (H=2048, I=768, gs=32, f16 scales), so gate|up on the
+    integer dot, down on the LDS ring and the tree combine over 384 pairs;
+    48 distinct experts, each evaluated 8 times, against float64."""
+    rng = np.random.default_rng(384)
+    H, I, gs = 2048, 768, 32
+    pool = [X.synthetic_expert(H, I, "int4", gs, rng) for _ in range(48)]
+    mats = [oracle_expert(e) for e in pool]
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    items, oitems = [], []
+    for j in rng.permutation(np.repeat(np.arange(48), 8)):
+        rows = np.zeros(1, np.int32)
+        w = rng.random(1).astype(np.float32)
+        items.append((kernels.q4_expert_ptrs(pool[j]), rows, w))
+        oitems.append((lambda xr, m=mats[j]: R.expert_exact(xr, *m), rows, w))
+    out = np.zeros_like(x)
+    kernels.moe_q4(x, items, H, I, gs, out)
+    close(out, R.moe_q4(x, oitems, np.zeros(x.shape)))
+
+
 @pytest.mark.parametrize("k,counts", [(384, (384,)), (100, (100, 21, 8, 9, 1))])
 def test_rows_with_many_pairs(kernels, k, counts):
     """A row in many experts' pair lists (one token's 48 layers x top-8 in one
