@@ -124,8 +124,9 @@ struct FmtQ4 {
 //  * Dot: acc_k = sum over the 4 words of dot8(w, limb k), exact; the chunk's
 //    sum (u - 8) * x_int = sum acc_k 16^k, formed as two exact 3-limb
 //    integers joined by one rounding, then scaled by 2^-S.
-// Each product term is off by at most |u - 8| * 2^-(S+1) <= 8 * 2^-23 of the
-// chunk's largest |x|, and a one-hot x is exact.
+// Each product term is off by at most |u - 8| * 2^-(S+1) <= 8 * 2^-22 of the
+// chunk's largest |x| m (2^-(S+1) <= 2^-22 m, as m >= 2^(21-S)), and a
+// one-hot x is exact.
 struct FmtQ4D {
   static constexpr int VALS = 32;
   static constexpr int XR = 25;
@@ -167,9 +168,13 @@ struct FmtQ4D {
   __device__ static void load_x(const XSrc& xs, int chunk, float* xr) {
     float v[32];
     xs.run<32>(chunk * 32, v);
-    float m = 0.f;
+    // m: the largest |x| (fmaxf drops NaN); z: 0, or NaN when a value is not finite
+    float m = 0.f, z = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+    for (int i = 0; i < 32; ++i) {
+      m = fmaxf(m, fabsf(v[i]));
+      z += v[i] - v[i];
+    }
     const int S = 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0);
     uint32_t xb[32];
 #pragma unroll
@@ -181,7 +186,7 @@ struct FmtQ4D {
 #pragma unroll
       for (int k = 0; k < 6; ++k) xr[6 * j + k] = __builtin_bit_cast(float, w[k]);
     }
-    xr[24] = __builtin_ldexpf(1.0f, -S) + (m - m);  // m - m: NaN for a non-finite chunk
+    xr[24] = __builtin_ldexpf(1.0f, -S) + z;  // NaN for a chunk holding Inf or NaN
   }
 
   // sum over the chunk of (u - 8) * x, u the unsigned nibble

@@ -341,9 +341,12 @@ struct Q4W24D {
     for (int k = 0; k < 3; ++k) {
       float v[16];
       xs.run<16>(chunk * 48 + 16 * k, v);
-      float m = 0.f;
+      float m = 0.f, z = 0.f;  // z: 0, or NaN when a value is not finite (fmaxf drops NaN)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+      for (int i = 0; i < 16; ++i) {
+        m = fmaxf(m, fabsf(v[i]));
+        z += v[i] - v[i];
+      }
       const int S = 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0);
       uint32_t xb[16];
 #pragma unroll
@@ -355,7 +358,7 @@ struct Q4W24D {
 #pragma unroll
         for (int l = 0; l < 6; ++l) xr[12 * k + 6 * h + l] = __builtin_bit_cast(float, w[l]);
       }
-      xr[36 + k] = __builtin_ldexpf(1.0f, -S) + (m - m);  // m - m: NaN for a non-finite sub-chunk
+      xr[36 + k] = __builtin_ldexpf(1.0f, -S) + z;  // NaN for a sub-chunk holding Inf or NaN
     }
   }
 
@@ -632,8 +635,11 @@ __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, in
   const MatRef M = resolve(job, mat);
   if (ring_stride > 0 && p1 - p0 == 1 && aligned(M.w, 16) && aligned(M.s, 16)) {
     const uint32_t sst = w24_ring_scales(L, sh.G, M.s_f16 != 0);
-    if (sst % 16 == 0 && (uint32_t)kW24Stage + sst <= (uint32_t)ring_stride &&
-        (uint32_t)sh.O * (uint32_t)sh.G * (M.s_f16 ? 2u : 4u) >= 16u) {
+    // the scale loads are whole 16-byte pieces clamped to the matrix's last
+    // one: the matrix's scale bytes must end on a 16-byte boundary, or the
+    // tail of its last row would be read from the wrong place
+    const uint32_t sall = (uint32_t)sh.O * (uint32_t)sh.G * (M.s_f16 ? 2u : 4u);
+    if (sst % 16 == 0 && (uint32_t)kW24Stage + sst <= (uint32_t)ring_stride && sall >= 16u && sall % 16u == 0) {
       uint8_t* ring = w24_ring + (size_t)wave * NS * ring_stride;
       if (M.s_f16) mv_w24_ring<F, L, NS, true>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
       else mv_w24_ring<F, L, NS, false>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);

@@ -448,7 +448,11 @@ class ExpertStore:
         groups = list(groups)
         xd = kernels.to_device(x, torch.float32)
         out = torch.zeros(xd.shape, dtype=torch.float32, device=xd.device)
-        items, H, shape = [], xd.shape[1], None
+        # ``keep`` holds every expert whose device addresses go into the layer
+        # call until it is enqueued: a later get() may drop an earlier expert
+        # from the bounded tiers, and its freed blocks could be handed to the
+        # next upload before the call reads them (moelan/experts.py:732-735)
+        items, keep, H, shape = [], [], xd.shape[1], None
         big = []
         ys, yrows, yw = [], [], []
         for expert, rows, weights in groups:
@@ -463,6 +467,7 @@ class ExpertStore:
                 continue
             if kernels.FUSED and e.fused and (shape is None or dims == shape):
                 shape = dims
+                keep.append(e)
                 items.append((e.fused, rows, weights))
                 continue
             rows_t = torch.as_tensor(np.asarray(rows, np.int64), device=xd.device)
@@ -482,6 +487,7 @@ class ExpertStore:
         kernels.combine(out, ys, yrows, yw)
         if items:
             kernels.moe_q4(xd, items, H, shape[0], shape[1], out)
+        del keep   # the call is enqueued: stream order protects the blocks from here on
         return out if kernels.is_device(x) else out.cpu().numpy()
 
     def layer_table(self, layer: int, num_experts: int):

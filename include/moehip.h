@@ -65,8 +65,10 @@ int moe_version(void);
  * usual expert shapes) each run of 32 (or 16) activations is taken as exact
  * fixed point rint(x * 2^S), S set by the run's largest |x|, and multiplied
  * with the nibbles exactly (integer dot products), then scaled by the group
- * scale in f32. Each product term is off by at most 8 * 2^-23 of that
- * largest |x|; a non-finite x makes the outputs that use it non-finite.
+ * scale in f32. Each product term is off by at most 8 * 2^-22 of that
+ * largest |x| (so a run holding an outlier 2^k times its other values keeps
+ * about 22 - k bits of them); an Inf or NaN in x makes the outputs that use
+ * it NaN.
  * Other shapes multiply in f32. */
 int moe_q4_matmul_t(const float* x, int n, const uint8_t* raw, const void* s, int s_f16, int O, int I, int gs,
                     int offset, float* y, void* stream);

@@ -186,3 +186,37 @@ def test_store_mixes_formats(kernels):
     got = store.compute(0, x, groups)
     want = R.store_compute(x, groups, lambda e, xr: R.expert_exact(xr, *oracle_expert(ex[(0, e)])))
     close(got, want)
+
+
+class _MappedSource:
+    """A zero-copy source (as a memory-mapped container): each load() builds a
+    new Expert, so an expert dropped from the store's bounded map tier takes
+    its device copy with it."""
+    zero_copy = True
+
+    def __init__(self, H, I, n, seed=0):
+        self.H, self.I, self.n, self.seed = H, I, n, seed
+
+    def has(self, key):
+        return key[0] == 0 and 0 <= key[1] < self.n
+
+    def load(self, key):
+        return X.synthetic_expert(self.H, self.I, "int4", 32, np.random.default_rng(self.seed + key[1]))
+
+
+@pytest.mark.parametrize("map_size", [1, 2])
+def test_store_keeps_fused_experts_alive_until_the_call(kernels, map_size):
+    """With a map tier smaller than a layer's experts, each get() drops an
+    earlier expert (and its device copy) while the next one uploads; the layer
+    call must still read every expert's own weights (the store holds them
+    until the call is enqueued, as moelan/experts.py:732-735)."""
+    H, I, n = 512, 256, 6
+    src = _MappedSource(H, I, n, seed=40)
+    store = X.ExpertStore([src], fmt="int4", map_size=map_size)
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((3, H)).astype(np.float32)
+    groups = groups_for(rng, [(e, [e % 3] if e % 2 else [0, 2]) for e in range(n)])
+    got = store.compute(0, x, groups)
+    assert len(store.mapped) == map_size
+    want = R.store_compute(x, groups, lambda e, xr: R.expert_exact(xr, *oracle_expert(src.load((0, e)))))
+    close(got, want)

@@ -64,8 +64,38 @@ def near_tie_rows(logits, k, rel=4e-7):
     return set(np.nonzero(gap < rel)[0].tolist())
 
 
+def assert_tie_swaps_only(logits, gidx, ridx, k, rel=4e-7):
+    """Where the device's picks differ from the oracle's, they differ only
+    inside a near-tie: the picks outside the experts whose probability is
+    within `rel` of the k-th one agree, every device pick outside that group is
+    an oracle pick, and the device's picks come in descending probability
+    order (up to `rel`). Returns the rows that differ."""
+    p = R.softmax(np.asarray(logits, np.float32)).astype(np.float64)
+    diff = [r for r in range(len(logits)) if not np.array_equal(gidx[r], ridx[r])]
+    for r in diff:
+        pk = np.sort(p[r])[::-1][k - 1]
+        group = set(np.nonzero(np.abs(p[r] - pk) <= rel * pk)[0].tolist())
+        assert len(group) >= 2, f"row {r}: picks {gidx[r]} vs {ridx[r]} without a near-tie"
+        g, o = set(gidx[r].tolist()), set(ridx[r].tolist())
+        assert g - group == o - group, f"row {r}: {sorted(g)} vs {sorted(o)} beyond the tie {sorted(group)}"
+        assert len(g) == k and g <= o | group
+        pg = p[r][gidx[r]]
+        assert np.all(pg[1:] <= pg[:-1] * (1 + rel)), f"row {r}: picks not in descending order"
+    return diff
+
+
+def weights_of(logits, idx, normalize):
+    """The oracle's f32 route weights for the given picks (moelan/model.py:160-167)."""
+    p = R.softmax(np.asarray(logits, np.float32))
+    w = np.take_along_axis(p, np.asarray(idx, np.int64), 1)
+    return (w / w.sum(1, keepdims=True)).astype(np.float32) if normalize else w
+
+
 @pytest.mark.parametrize("E,k", [(128, 8), (64, 4), (256, 8), (8, 2), (60, 6)])
 def test_route_matches_oracle_on_identical_logits(kernels, E, k):
+    """Picks bit-exact with the oracle's, except inside near-ties (f32 softmax
+    rounding may order those either way), where only the tied experts may
+    trade places; weights then match the oracle's for the device's picks."""
     rng = np.random.default_rng(E + k)
     logits = rng.standard_normal((700, E)).astype(np.float32) * 2
     logits[3] = 0.25                        # all tied: lowest ids win
@@ -74,11 +104,10 @@ def test_route_matches_oracle_on_identical_logits(kernels, E, k):
         idx, w = kernels.route(logits, k, normalize)
         ridx, rw = R.route(logits, k, normalize)
         ties = near_tie_rows(logits, k)
-        ok = [r for r in range(len(logits)) if r not in ties]
-        assert np.array_equal(idx[ok], ridx[ok])
+        diff = assert_tie_swaps_only(logits, idx, ridx, k)
+        assert set(diff) <= ties and len(ties) <= 2
         assert idx[3].tolist() == list(range(k))
-        np.testing.assert_allclose(w[ok], rw[ok], rtol=2e-6, atol=1e-7)
-        assert len(ties) <= 2
+        np.testing.assert_allclose(w, weights_of(logits, idx, normalize), rtol=2e-6, atol=1e-7)
 
 
 @pytest.mark.parametrize("T,k,E", [(512, 8, 128), (1792, 8, 128), (4000, 8, 128), (37, 4, 16), (1, 2, 8),
@@ -170,14 +199,17 @@ def test_qwen3_30b_prefill_layer(kernels, c4_experts):
     Rw = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
     table = kernels.expert_table(c4_experts)
     out = kernels.prefill_layer(x, Rw, table, k, True, H, I, 32)
-    # the oracle routes on the device's logits (routing is checked separately)
+    # the oracle routes on the device's logits (routing is checked separately);
+    # tokens whose picks differ from the oracle's only inside a near-tie are
+    # compared with the device's picks and the oracle's weights for them
     logits = kernels.router_logits(x, Rw)
-    ridx, rw = R.route(logits, k, True)
+    ridx, _ = R.route(logits, k, True)
     gidx, _ = kernels.route(logits, k, True)
-    ties = near_tie_rows(logits, k)
-    assert len(ties) <= 2
-    ok = [t for t in range(T) if t not in ties and np.array_equal(gidx[t], ridx[t])]
-    assert len(ok) >= T - 2
+    diff = assert_tie_swaps_only(logits, gidx, ridx, k)
+    assert len(diff) <= 2
+    ridx[diff] = gidx[diff]
+    rw = weights_of(logits, ridx, True)
+    ok = None   # every token
     ref = np.zeros((T, H))
     for e in range(E):
         sel = np.nonzero((ridx == e).any(1))[0]
