@@ -62,6 +62,8 @@ SIGNATURES = {
     "moe_q4_gemm": (c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "moe_q4_layer": (c_int, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I,
                              _I, _I, _I, _I, _P, _Z, _P]),
+    "moe_q4_layer_noalloc": (c_int, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I,
+                                     _I, _I, _I, _I, _P]),
     "moe_q4_layer_i8_workspace": (c_size_t, [_I, _I, _I, _I]),
     "moe_q4_layer_i8": (c_int, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I,
                                 _I, _I, _I, _I, _P, _Z, _P]),

@@ -187,43 +187,83 @@ MOE_API size_t moe_q4_layer_workspace(int P, int H, int I) {
   return q4_layer_workspace(P, H, I);
 }
 
+namespace moe {
+// the argument checks of moe_q4_layer and moe_q4_layer_noalloc (who: the
+// caller's name); fills everything but the workspace. *empty: nothing to do.
+static int q4_layer_args(const char* who, const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k,
+                         const int* poff, const int* prow, const float* pw, int P, const int* rrow, const int* rptr,
+                         const int* rpair, int nr, float* out, int ldo, int H, int I, int gs, int max_rows,
+                         Q4LayerArgs* a, bool* empty) {
+  REQUIRE(H > 0 && I > 0 && H % 2 == 0 && I % 2 == 0, "%s: H=%d and I=%d must be positive and even", who, H, I);
+  REQUIRE(gs > 0 && gs % 2 == 0 && H % gs == 0 && I % gs == 0, "%s: group size %d must divide H=%d and I=%d", who,
+          gs, H, I);
+  REQUIRE(k >= 0 && P >= 0 && nr >= 0, "%s: k=%d P=%d nr=%d", who, k, P, nr);
+  *empty = k == 0 || P == 0;
+  if (*empty) return MOE_OK;
+  REQUIRE(max_rows > 0 && max_rows <= P, "%s: max_rows=%d for P=%d", who, max_rows, P);
+  REQUIRE(ldx >= H && ldo >= H, "%s: ldx=%d ldo=%d must be >= H=%d", who, ldx, ldo, H);
+  REQUIRE(x && table && poff && prow && pw && rrow && rptr && rpair && out, "%s: null pointer", who);
+  *a = Q4LayerArgs{};
+  a->x = x;
+  a->ldx = ldx;
+  a->table = reinterpret_cast<const ExpertDesc*>(table);
+  a->eidx = eidx;
+  a->k = k;
+  a->poff = poff;
+  a->prow = prow;
+  a->pw = pw;
+  a->P = P;
+  a->rrow = rrow;
+  a->rptr = rptr;
+  a->rpair = rpair;
+  a->nr = nr;
+  a->out = out;
+  a->ldo = ldo;
+  a->H = H;
+  a->I = I;
+  a->gs = gs;
+  a->max_rows = max_rows;
+  return MOE_OK;
+}
+}  // namespace moe
+
 MOE_API int moe_q4_layer(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k,
                          const int* poff, const int* prow, const float* pw, int P, const int* rrow, const int* rptr,
                          const int* rpair, int nr, float* out, int ldo, int H, int I, int gs, int max_rows,
                          void* workspace, size_t ws_bytes, void* stream) {
-  REQUIRE(H > 0 && I > 0 && H % 2 == 0 && I % 2 == 0, "moe_q4_layer: H=%d and I=%d must be positive and even", H, I);
-  REQUIRE(gs > 0 && gs % 2 == 0 && H % gs == 0 && I % gs == 0, "moe_q4_layer: group size %d must divide H=%d and I=%d",
-          gs, H, I);
-  REQUIRE(k >= 0 && P >= 0 && nr >= 0, "moe_q4_layer: k=%d P=%d nr=%d", k, P, nr);
-  if (k == 0 || P == 0) return MOE_OK;
-  REQUIRE(max_rows > 0 && max_rows <= P, "moe_q4_layer: max_rows=%d for P=%d", max_rows, P);
-  REQUIRE(ldx >= H && ldo >= H, "moe_q4_layer: ldx=%d ldo=%d must be >= H=%d", ldx, ldo, H);
-  REQUIRE(x && table && poff && prow && pw && rrow && rptr && rpair && out, "moe_q4_layer: null pointer");
+  Q4LayerArgs a;
+  bool empty = false;
+  if (int rc = q4_layer_args("moe_q4_layer", x, ldx, table, eidx, k, poff, prow, pw, P, rrow, rptr, rpair, nr, out,
+                             ldo, H, I, gs, max_rows, &a, &empty))
+    return rc;
+  if (empty) return MOE_OK;
   const size_t need = q4_layer_workspace(P, H, I);
   if (workspace == nullptr || ws_bytes < need)
     return set_error(MOE_EWORKSPACE, "moe_q4_layer: workspace of %zu bytes, %zu needed", ws_bytes, need);
   REQUIRE(aligned(workspace, 16), "moe_q4_layer: workspace must be 16-byte aligned");
-  Q4LayerArgs a{};
-  a.x = x;
-  a.ldx = ldx;
-  a.table = reinterpret_cast<const ExpertDesc*>(table);
-  a.eidx = eidx;
-  a.k = k;
-  a.poff = poff;
-  a.prow = prow;
-  a.pw = pw;
-  a.P = P;
-  a.rrow = rrow;
-  a.rptr = rptr;
-  a.rpair = rpair;
-  a.nr = nr;
-  a.out = out;
-  a.ldo = ldo;
-  a.H = H;
-  a.I = I;
-  a.gs = gs;
-  a.max_rows = max_rows;
   a.workspace = workspace;
+  return run_q4_layer(a, as_stream(stream));
+}
+
+MOE_API int moe_q4_layer_noalloc(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k,
+                                 const int* poff, const int* prow, const float* pw, int P, const int* rrow,
+                                 const int* rptr, const int* rpair, int nr, float* out, int ldo, int H, int I, int gs,
+                                 int max_rows, void* stream) {
+  Q4LayerArgs a;
+  bool empty = false;
+  if (int rc = q4_layer_args("moe_q4_layer_noalloc", x, ldx, table, eidx, k, poff, prow, pw, P, rrow, rptr, rpair, nr,
+                             out, ldo, H, I, gs, max_rows, &a, &empty))
+    return rc;
+  if (empty) return MOE_OK;
+  const size_t need = q4_layer_workspace(P, H, I);
+  if (need > kLayerScratchBytes)
+    return set_error(MOE_EWORKSPACE,
+                     "moe_q4_layer_noalloc: %d pairs at H=%d, I=%d need %zu bytes of scratch, more than the %zu the "
+                     "library holds (P * (2I + H) * 4 must not exceed it; use moe_q4_layer with a workspace)",
+                     P, H, I, need, kLayerScratchBytes);
+  void* ws = nullptr;
+  if (int rc = layer_scratch(&ws)) return rc;
+  a.workspace = ws;
   return run_q4_layer(a, as_stream(stream));
 }
 

@@ -25,6 +25,10 @@ struct Q4LayerArgs {
 };
 
 size_t q4_layer_workspace(int P, int H, int I);
+// bytes of the library-held scratch the workspace-free layer call uses (per device)
+constexpr size_t kLayerScratchBytes = (size_t)32 << 20;
+// that scratch's device address on the current device (looked up once per device)
+int layer_scratch(void** ptr);
 int run_q4_layer(const Q4LayerArgs& a, hipStream_t st);
 // the same call with activations rounded to int8 per group (gs a multiple of 64)
 size_t q4i8_layer_workspace(int P, int H, int I, int gs);

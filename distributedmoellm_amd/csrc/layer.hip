@@ -5,11 +5,45 @@
 //   3. weighted sum per touched row, in runs of 8 pairs in pair order
 //      (expert order), then added to out: out[r] += sum_p pw[p] * y[p]
 //      (deterministic)
+#include <mutex>
+
 #include "common.h"
 #include "matvec.h"
 #include "layer.h"
 
 namespace moe {
+
+// ------------------------------------------------------------------ library-held scratch
+//
+// The workspace-free layer call (moe_q4_layer_noalloc) keeps its h and y in
+// this array instead of a caller's workspace. Each device the library runs
+// on holds its own copy from when the code object is loaded there until the
+// process ends. In host code `scratch` names a host-side stand-in, not device
+// memory: its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that address is
+// used. Every call on a device shares that device's array, so calls that
+// overlap on one device (other streams, other threads) race.
+static __device__ __align__(256) uint8_t scratch[kLayerScratchBytes];
+
+int layer_scratch(void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(MOE_EHIP, "layer scratch: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(MOE_EUNSUPPORTED, "layer scratch: device %d", dev);
+  std::lock_guard<std::mutex> g(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(MOE_EHIP, "layer scratch: hipGetSymbolAddress on device %d: %s", dev, hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return MOE_OK;
+}
 
 // part = sum over the row's pairs of w * y; then out[row] += part. A block
 // takes one touched row and 256 columns (64 threads x 4 columns); its 4 waves

@@ -57,6 +57,10 @@ def test_struct_layout():
     (lambda L: L.moe_gguf_dequant(1, 8, 8, 33, 1, None), "multiple of 32"),
     (lambda L: L.moe_q4_layer(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 32, 1,
                               1, 10, None), "workspace"),
+    (lambda L: L.moe_q4_layer_noalloc(1, 4096, 1, None, 1, 1, 1, 1, 2000, 1, 1, 1, 1, 1, 4096, 4096, 1536, 32, 1,
+                                      None), "scratch"),
+    (lambda L: L.moe_q4_layer_noalloc(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 24, 1,
+                                      None), "group size 24"),
     (lambda L: L.moe_q4_layer(1, 64, 1, None, 1, 1, 1, 1, 4, 1, 1, 1, 1, 1, 64, 64, 32, 24, 1,
                               1, 10, None), "group size 24"),
     (lambda L: L.moe_combine(1, 8, 1, 1, 1, 1, 1, 0, 1, 8, 16, None), "ldy=8"),
