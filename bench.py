@@ -458,43 +458,87 @@ def zipf_calls(rng, B: int, E: int = 128, k: int = 8, s: float = 1.1):
     return eidx, rows, ws
 
 
-def stack_decode(args, L):
-    """Qwen3-235B-A22B-shaped expert stack resident in HBM, decode steps at B = 1, 8, 32."""
+def stack_decode(args, L, batches=(1, 8, 32)):
+    """Qwen3-235B-A22B-shaped expert stack resident in HBM (94 layers x 128
+    experts, H=4096, I=1536, int4 group 32, f16 scales, 119 GiB), one
+    continuous-batching decode step per timed iteration at B tokens: 94
+    layer calls in sequence (moe_q4_layer), each on the previous layer's output
+    (the residual stream x += MoE(x), in place), top-8 routing from a seeded
+    Zipf(1.1) expert popularity per layer. Bytes per step: the packed weights
+    and scales of every distinct (layer, expert) touched, plus activations."""
     import torch
     H, I, gs, E, layers = 4096, 1536, 32, 128, 94
     log(f"stack: {layers} layers x {E} experts H={H} I={I} ({layers * E * expert_bytes(H, I, gs) / 2**30:.1f} GiB)")
     pools = [Int4Pool(E, H, I, gs, seed=100 + l) for l in range(layers)]
     stream = torch.cuda.current_stream().cuda_stream
     res = {}
-    for B in (1, 8, 32):
+    for B in batches:
         rng = np.random.default_rng(B)
         nvar = 2
         calls = Calls([zipf_calls(rng, B) for _ in range(nvar * layers)])
         dist = np.array([calls.items[i]["k"] for i in range(nvar * layers)]).reshape(nvar, layers)
-        step_bytes = dist.sum(1) * expert_bytes(H, I, gs)
+        rows_max = max(c["max_rows"] for c in calls.items)
+        step_bytes = dist.sum(1) * expert_bytes(H, I, gs) + 2 * layers * B * H * 4
         Pmax = max(c["P"] for c in calls.items)
+        need = L.moe_q4_layer_workspace(Pmax, H, I)
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
         x = torch.randn((B, H), device="cuda")
-        out = torch.zeros((B, H), device="cuda")
-        h = torch.empty((Pmax, 2 * I), device="cuda")
-        y = torch.empty((Pmax, H), device="cuda")
 
-        def step(v):
+        def step(v, stream=stream):
             for l in range(layers):
-                run_layer(L, pools[l], x, out, h, y, calls.items[v * layers + l], stream)
+                c = calls.items[v * layers + l]
+                rc = L.moe_q4_layer(x.data_ptr(), H, pools[l].table.data_ptr(), c["eidx"], c["k"], c["poff"],
+                                    c["prow"], c["pw"], c["P"], c["rrow"], c["rptr"], c["rpair"], c["nr"],
+                                    x.data_ptr(), H, H, I, gs, c["max_rows"], ws.data_ptr(), need, stream)
+                if rc:
+                    from distributedmoellm_amd import _lib
+                    raise RuntimeError(_lib.last_error())
         for v in range(nvar):
+            x.normal_()
             step(v)
         torch.cuda.synchronize()
-        nsteps = max(2, args.steps // 2)
-        t0 = time.perf_counter()
-        for s in range(nsteps):
-            step(s % nvar)
+        nsteps = max(4, min(args.steps, 20))
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
+        for s_ in range(nsteps):
+            x.normal_()          # a fresh token batch: outside the timed events
+            evs[s_][0].record()
+            step(s_ % nvar)
+            evs[s_][1].record()
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) / nsteps * 1e3
+        ms = float(np.median([a.elapsed_time(b) for a, b in evs]))
+        # the same steps captured as HIP graphs (one per routing variant) and replayed
+        graphs = []
+        for v in range(nvar):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step(v, torch.cuda.current_stream().cuda_stream)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        gevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
+        for s_ in range(nsteps):
+            x.normal_()
+            gevs[s_][0].record()
+            graphs[s_ % nvar].replay()
+            gevs[s_][1].record()
+        torch.cuda.synchronize()
+        ms_graph = float(np.median([a.elapsed_time(b) for a, b in gevs]))
+        del graphs
         avg_bytes = float(step_bytes.mean())
-        res[f"B{B}"] = dict(ms_per_step=ms, gbs=avg_bytes / (ms / 1e3) / 1e9, bytes_per_step=avg_bytes,
-                            experts_per_layer=float(dist.mean()),
-                            roofline_ms=avg_bytes / (HBM_PEAK_GBS * 1e9) * 1e3)
-        log(f"stack B={B}: {ms:.3f} ms/step, {res[f'B{B}']['gbs']:.0f} GB/s, {dist.mean():.1f} experts/layer")
+        key = f"B{B}"
+        res[key] = dict(ms_per_step=ms, ms_per_step_graph=ms_graph, gbs=avg_bytes / (ms / 1e3) / 1e9,
+                        gbs_graph=avg_bytes / (ms_graph / 1e3) / 1e9, bytes_per_step=avg_bytes,
+                        hbm_frac=avg_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+                        experts_per_layer=float(dist.mean()), max_rows_per_expert=int(rows_max),
+                        peak_ms=avg_bytes / (HBM_PEAK_GBS * 1e9) * 1e3,
+                        target_ms_70pct=avg_bytes / (0.7 * HBM_PEAK_GBS * 1e9) * 1e3,
+                        launches_per_layer=3 if rows_max == 1 else 5)
+        log(f"stack B={B}: {ms:.3f} ms/step ({ms_graph:.3f} as a graph), {res[key]['gbs']:.0f} GB/s "
+            f"({res[key]['hbm_frac'] * 100:.1f}% of HBM), "
+            f"{dist.mean():.1f} experts/layer, hottest {rows_max} rows")
+        del ws
+    res["workload"] = ("Qwen3-235B-A22B-shaped stack: 94 sequential layer calls per step (x += MoE(x)), 128 experts "
+                       "a layer, H=4096 I=1536 int4 g32 f16 scales (119 GiB resident), top-8 Zipf(1.1) routing; "
+                       "median of timed steps, HIP events")
     del pools
     torch.cuda.empty_cache()
     return res
@@ -593,6 +637,7 @@ def main() -> int:
                          "(each has its own --only part; kept out of the default run so that the default "
                          "command's kernel trace holds only the headline launches)")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
+    ap.add_argument("--batches", default="1,8,32", help="token batches of the 235B-shaped stack decode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, wire, residency, prefill, copy "
                                                 "(for counter and trace runs)")
@@ -626,6 +671,8 @@ def main() -> int:
             res["wire"] = wire_codec(args, L)
         if "residency" in only:
             res["residency"] = residency(args, L)
+        if "stack" in only:
+            res["stack"] = stack_decode(args, L, tuple(int(b) for b in args.batches.split(",")))
         if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
             import torch
             a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)

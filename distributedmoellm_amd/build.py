@@ -36,6 +36,11 @@ def hipcc() -> str:
     return "hipcc"
 
 
+# per-source additions: the multi-row GEMM wants its MFMA results in VGPRs
+# (the compiler's default puts them in AGPRs and copies them back one by one)
+EXTRA_FLAGS = {"rows.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
@@ -50,7 +55,7 @@ def build(verbose: bool = True) -> Path:
     t0 = time.time()
     with tempfile.TemporaryDirectory(prefix="moehip-") as tmpdir:
         objs = [Path(tmpdir) / (src.stem + ".o") for src in srcs]
-        procs = [subprocess.Popen([hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)],
+        procs = [subprocess.Popen([hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)],
                                   stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
                  for src, obj in zip(srcs, objs)]
         failed = []

@@ -37,7 +37,9 @@ int run_silu_mul(const float* h, int ldh, int n, int I, float* a, int lda, hipSt
 int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
                 float* out, int ldo, int H, hipStream_t st);
 // the same sum in one launch: a block per (row, 16 columns), 64 pair lanes added by a fixed tree
+// (P: the call's pairs; with at most 32 a touched row on average each row is
+// summed by one thread per column quad in list order instead)
 int run_combine_runs(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair, int nr,
-                     int max_pairs, float* out, int ldo, int H, hipStream_t st);
+                     int max_pairs, float* out, int ldo, int H, hipStream_t st, int P = 0);
 
 }  // namespace moe

@@ -6,12 +6,24 @@
 //      (expert order), then added to out: out[r] += sum_p pw[p] * y[p]
 //      (deterministic)
 #include <mutex>
+#include <stdlib.h>
 
 #include "common.h"
 #include "matvec.h"
 #include "layer.h"
+#include "rows.h"
 
 namespace moe {
+
+// MOEHIP_ROWS=0 keeps experts with several rows on the mat-vec kernels (a
+// measurement switch)
+static bool rows_disabled() {
+  static const bool off = [] {
+    const char* e = getenv("MOEHIP_ROWS");
+    return e && e[0] == '0';
+  }();
+  return off;
+}
 
 // ------------------------------------------------------------------ library-held scratch
 //
@@ -170,21 +182,116 @@ __global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int l
   }
 }
 
-// max_pairs: an upper bound of the pairs of one row
+// Few pairs a row (a decode step's top-k): a thread takes 4 columns of one
+// row and adds the row's pairs in list order (ascending), then adds the sum
+// to out. Fixed order, no atomics; y is only read.
+__global__ __launch_bounds__(256) void combine_rows_kernel(const float* y, int ldy, const float* pw, const int* rrow,
+                                                           const int* rptr, const int* rpair, float* out, int ldo,
+                                                           int H) {
+  const int i = blockIdx.y;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= H) return;
+  const int q0 = rptr[i], q1 = rptr[i + 1];
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  int q = q0;
+  for (; q + 4 <= q1; q += 4) {  // four loads in flight, added in list order
+    float4 v[4];
+    float w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = rpair[q + u];
+      w[u] = pw[p];
+      v[u] = *reinterpret_cast<const float4*>(y + (size_t)p * ldy + c);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      a.x += w[u] * v[u].x;
+      a.y += w[u] * v[u].y;
+      a.z += w[u] * v[u].z;
+      a.w += w[u] * v[u].w;
+    }
+  }
+  for (; q < q1; ++q) {
+    const int p = rpair[q];
+    const float w = pw[p];
+    const float4 v = *reinterpret_cast<const float4*>(y + (size_t)p * ldy + c);
+    a.x += w * v.x;
+    a.y += w * v.y;
+    a.z += w * v.z;
+    a.w += w * v.w;
+  }
+  float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+  float4 o = *dst;
+  o.x += a.x;
+  o.y += a.y;
+  o.z += a.z;
+  o.w += a.w;
+  *dst = o;
+}
+
+// max_pairs: an upper bound of the pairs of one row; P: all pairs of the call
 int run_combine_runs(float* y, int ldy, const float* pw, const int* rrow, const int* rptr, const int* rpair,
-                            int nr, int max_pairs, float* out, int ldo, int H, hipStream_t st) {
+                            int nr, int max_pairs, float* out, int ldo, int H, hipStream_t st, int P) {
   if (nr <= 0) return MOE_OK;
   const bool vec4 = H % 4 == 0 && ldy % 4 == 0 && ldo % 4 == 0 && aligned(y, 16) && aligned(out, 16);
   if (!vec4) return run_combine(y, ldy, pw, rrow, rptr, rpair, nr, out, ldo, H, st);
+  if (P > 0 && P <= 32 * nr && nr <= 65535) {  // few pairs a row on average: one thread a row's column quad
+    hipLaunchKernelGGL(combine_rows_kernel, dim3((H / 4 + 255) / 256, nr), dim3(256), 0, st, y, ldy, pw, rrow, rptr,
+                       rpair, out, ldo, H);
+    return check_launch("weighted combine");
+  }
   (void)max_pairs;  // the tree takes any number of pairs a row
   hipLaunchKernelGGL(combine_tree_kernel, dim3((H + 15) / 16, nr < 65535 ? nr : 65535), dim3(256), 0, st, y, ldy, pw,
                      rrow, rptr, rpair, nr, out, ldo, H);
   return check_launch("weighted combine");
 }
 
-size_t q4_layer_workspace(int P, int H, int I) { return (size_t)P * (2 * (size_t)I + H) * sizeof(float); }
+// The workspace: h [P, 2I] f32, y [P, H] f32, then (for shapes the rows GEMM
+// takes) its activation limbs, each piece 256-byte aligned.
+static size_t hy_bytes(int P, int H, int I) {
+  return ((size_t)P * (2 * (size_t)I + H) * sizeof(float) + 255) / 256 * 256;
+}
+
+size_t q4_layer_workspace(int P, int H, int I) {
+  size_t n = hy_bytes(P, H, I);
+  if (H % 256 == 0 && I % 256 == 0) n += rows_workspace(P, H, I);
+  return n;
+}
+
+// Experts with several rows each: each weight row read once per pass of up to
+// 8 rows, on integer MFMA (rows.hip); the same combine.
+static int run_q4_layer_rows(const Q4LayerArgs& a, hipStream_t st) {
+  float* h = reinterpret_cast<float*>(a.workspace);
+  float* y = h + (size_t)a.P * 2 * a.I;
+  const RowsSpace rs = rows_layout((char*)a.workspace + hy_bytes(a.P, a.H, a.I), a.P, a.H, a.I);
+  int rc = run_rows_prep(a.x, a.ldx, a.prow, a.poff, a.k, a.P, a.H, 0, rs, rs.agu, st);
+  if (rc) return rc;
+  MVJob j1{};
+  j1.y = h;
+  j1.ldy = 2 * a.I;
+  j1.seg = a.poff;
+  j1.experts = a.table;
+  j1.eidx = a.eidx;
+  j1.which = 0;
+  rc = run_rows_gemm(j1, a.k, 2 * a.I, a.H, a.max_rows, rs, rs.agu, st);
+  if (rc) return rc;
+  rc = run_rows_prep(h, 2 * a.I, nullptr, a.poff, a.k, a.P, a.I, a.I, rs, rs.adn, st);
+  if (rc) return rc;
+  MVJob j2{};
+  j2.y = y;
+  j2.ldy = a.H;
+  j2.seg = a.poff;
+  j2.experts = a.table;
+  j2.eidx = a.eidx;
+  j2.which = 1;
+  rc = run_rows_gemm(j2, a.k, a.H, a.I, a.max_rows, rs, rs.adn, st);
+  if (rc) return rc;
+  return run_combine_runs(y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st,
+                          a.P);
+}
 
 int run_q4_layer(const Q4LayerArgs& a, hipStream_t st) {
+  if (a.max_rows >= 2 && rows_gemm_ok(a.H, a.I, a.gs) && !rows_disabled()) return run_q4_layer_rows(a, st);
   float* h = reinterpret_cast<float*>(a.workspace);
   float* y = h + (size_t)a.P * 2 * a.I;
   MVShape s1, s2;
@@ -220,7 +327,8 @@ int run_q4_layer(const Q4LayerArgs& a, hipStream_t st) {
   if (rc) return rc;
 
   // a row has at most one pair per expert of the call
-  return run_combine_runs(y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st);
+  return run_combine_runs(y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st,
+                          a.P);
 }
 
 // The workspace of the int8-activation call, each piece 256-byte aligned:
@@ -296,7 +404,8 @@ int run_q4i8_layer(const Q4LayerArgs& a, hipStream_t st) {
   rc = run_matvec_q4i8(s2, j2, a.k, w.qa, w.da, w.sa, st);
   if (rc) return rc;
 
-  return run_combine_runs(w.y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H, st);
+  return run_combine_runs(w.y, a.H, a.pw, a.rrow, a.rptr, a.rpair, a.nr, a.k < a.P ? a.k : a.P, a.out, a.ldo, a.H,
+                          st, a.P);
 }
 
 }  // namespace moe
