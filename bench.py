@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the routed-expert path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--stack] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extras]
 
 Headline (one JSON line on stdout): int4 expert decode mat-vec HBM GB/s.
 A step is one token's 384 routed-expert evaluations at the Qwen3-30B-A3B
@@ -23,10 +23,14 @@ summary committed beside the kernel-trace summary
 WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain
 device copy of known size); null when that summary is absent.
 
-Extras in the same line: the Qwen3-30B-A3B-shaped MoE layer prefill (T=512)
-with its own CPU baseline; with --per-layer the same 384 evaluations as 48
-per-layer calls; with --stack the Qwen3-235B-A22B-shaped resident stack decode
-(94 layers x 128 experts, 119 GiB) at B = 1, 8, 32 with Zipf(1.1) routing.
+Extras in the same line, one per benchmark configuration: the
+Qwen3-235B-A22B-shaped resident stack decode (94 layers x 128 experts, 119 GiB,
+94 chained layer calls a step) at B = 1, 8, 32 with Zipf(1.1) routing; int8
+group-scaled experts at B = 1, 4, 16, 64; GGUF Q8_0 / Q4_K experts at B = 1, 32;
+the Qwen3-30B-A3B-shaped MoE layer prefill (T=512) with its own CPU baseline.
+With --per-layer the 384 evaluations also as 48 per-layer calls; --extras adds
+the group-64 int8-activation decode, every GGUF type's mat-vec, the wire codec
+and residency.
 """
 
 from __future__ import annotations
@@ -46,6 +50,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+FP32_PEAK_TFLOPS = 157.3
 TRAFFIC_SUMMARY = ROOT / "profiles" / "mv_fast_kernel_int4_decode_384experts.md"
 
 
@@ -304,6 +309,143 @@ def gguf_matvec(args, L, target_bytes: int = 256 << 20, cols: int = 2048):
     return res
 
 
+def _time_calls(fn, n, warm=3):
+    """Mean milliseconds of fn() over n calls, HIP events on the current stream."""
+    import torch
+    for _ in range(warm):
+        fn(0)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(n):
+        fn(i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / n
+
+
+def _check(rc):
+    if rc:
+        from distributedmoellm_amd import _lib
+        raise RuntimeError(_lib.last_error())
+
+
+def int8_c2(args, L, batches=(1, 4, 16, 64)):
+    """Group-scaled int8 experts (H=2048, I=768: gate|up [1536 x 2048], down
+    [2048 x 768], group 32, f16 scales |N(0,0.02)|/127, int8 uniform in
+    [-127, 127]) applied to B routed rows (moe_q8_matmul_t, the reference's
+    q8_matmul_t per matrix): per expert evaluation (two calls, experts cycled
+    through a 256-expert, 1.28 GB pool) and the kernel's rate on one stacked
+    gate|up matrix of all 256 experts (805 MB, one call). Bytes: int8 values +
+    f16 scales (5,013,504 per expert) + activations; flops 2 B 3 H I."""
+    import torch
+    H, I, gs, n = 2048, 768, 32, 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(21)
+    qgu = torch.randint(-127, 128, (n, 2 * I, H), dtype=torch.int8, device="cuda", generator=g)
+    qdn = torch.randint(-127, 128, (n, H, I), dtype=torch.int8, device="cuda", generator=g)
+    sgu = (torch.randn((n, 2 * I, H // gs), device="cuda", generator=g).abs_() * (0.02 / 127)).half()
+    sdn = (torch.randn((n, H, I // gs), device="cuda", generator=g).abs_() * (0.02 / 127)).half()
+    stream = torch.cuda.current_stream().cuda_stream
+    ebytes = 3 * H * I + 3 * H * I // gs * 2
+    res = {}
+    for B in batches:
+        x = torch.randn((B, H), device="cuda")
+        a = torch.randn((B, I), device="cuda")
+        ygu = torch.empty((B, 2 * I), device="cuda")
+        ydn = torch.empty((B, H), device="cuda")
+
+        def expert(i):
+            e = (i * 37) % n
+            _check(L.moe_q8_matmul_t(x.data_ptr(), B, qgu[e].data_ptr(), sgu[e].data_ptr(), 1, 2 * I, H, gs,
+                                     ygu.data_ptr(), stream))
+            _check(L.moe_q8_matmul_t(a.data_ptr(), B, qdn[e].data_ptr(), sdn[e].data_ptr(), 1, H, I, gs,
+                                     ydn.data_ptr(), stream))
+        ms = _time_calls(expert, 128)
+        byts = ebytes + B * (H + I) * 4 * 2
+        flops = 2.0 * B * 3 * H * I
+        ybig = torch.empty((B, n * 2 * I), device="cuda")
+
+        def stacked(i):
+            _check(L.moe_q8_matmul_t(x.data_ptr(), B, qgu.data_ptr(), sgu.data_ptr(), 1, n * 2 * I, H, gs,
+                                     ybig.data_ptr(), stream))
+        ms_big = _time_calls(stacked, 10)
+        big_bytes = n * 2 * I * (H + H // gs * 2) + B * (H + n * 2 * I) * 4
+        big_flops = 2.0 * B * n * 2 * I * H
+        res[f"B{B}"] = dict(us_per_expert=round(ms * 1e3, 2), gbs_per_expert=round(byts / ms / 1e6, 1),
+                            hbm_frac_per_expert=round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+                            fp32_frac_per_expert=round(flops / ms / 1e9 / FP32_PEAK_TFLOPS, 4),
+                            stacked_us=round(ms_big * 1e3, 1), stacked_gbs=round(big_bytes / ms_big / 1e6, 1),
+                            stacked_hbm_frac=round(big_bytes / ms_big / 1e6 / HBM_PEAK_GBS, 4),
+                            stacked_fp32_frac=round(big_flops / ms_big / 1e9 / FP32_PEAK_TFLOPS, 4),
+                            bound="hbm" if B <= 4 else "fp32")
+        log(f"int8 B={B}: {ms * 1e3:.1f} us/expert ({byts / ms / 1e6:.0f} GB/s), stacked gate|up "
+            f"{big_bytes / ms_big / 1e6:.0f} GB/s ({big_flops / ms_big / 1e9:.1f} TFLOP/s)")
+        del x, a, ygu, ydn, ybig
+    res["workload"] = ("C2: int8 group-32 experts H=2048 I=768, f16 scales, B routed rows; per expert = the two "
+                       "q8_matmul_t calls of an expert evaluation from a 256-expert (1.28 GB) pool; stacked = one "
+                       "call over all 256 experts' gate|up rows (805 MB)")
+    del qgu, qdn, sgu, sdn
+    torch.cuda.empty_cache()
+    return res
+
+
+def gguf_c3(args, L, batches=(1, 32)):
+    """GGUF experts at the Qwen3-30B-A3B shape: gate and up [768 x 2048] and
+    down [2048 x 768] in Q8_0 (34-byte blocks of 32) and Q4_K (144-byte
+    superblocks of 256), B routed rows (moe_gguf_matmul_t, the reference's
+    gguf_matmul_t per matrix): per expert evaluation (three calls) cycled
+    through a pool beyond the 256 MB MALL. Blocks are random bytes with their
+    f16 d (and dmin) fields set to |N(0, 0.01)|. Bytes: the blocks +
+    activations."""
+    import torch
+    H, I = 2048, 768
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for qt, name, n in ((8, "Q8_0", 128), (12, "Q4_K", 256)):
+        _, per, size = GGUF_TYPES[qt]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(31 + qt)
+
+        def blocks(O, cols):
+            raw = torch.randint(0, 256, (n, O, cols // per, size), dtype=torch.uint8, device="cuda", generator=g)
+            d = (torch.randn((n, O, cols // per), device="cuda", generator=g).abs_() * 0.01).half()
+            raw[..., 0:2] = d.view(torch.uint8).view(n, O, cols // per, 2)
+            if qt == 12:   # dmin
+                dm = (torch.randn((n, O, cols // per), device="cuda", generator=g).abs_() * 0.01).half()
+                raw[..., 2:4] = dm.view(torch.uint8).view(n, O, cols // per, 2)
+            return raw.view(n, O, cols // per * size)
+        gate, up, down = blocks(I, H), blocks(I, H), blocks(H, I)
+        ebytes = (2 * I * (H // per) + H * (I // per)) * size
+        for B in batches:
+            x = torch.randn((B, H), device="cuda")
+            a = torch.randn((B, I), device="cuda")
+            yg = torch.empty((B, I), device="cuda")
+            yu = torch.empty((B, I), device="cuda")
+            yd = torch.empty((B, H), device="cuda")
+
+            def expert(i):
+                e = (i * 37) % n
+                _check(L.moe_gguf_matmul_t(x.data_ptr(), B, gate[e].data_ptr(), qt, I, H, yg.data_ptr(), stream))
+                _check(L.moe_gguf_matmul_t(x.data_ptr(), B, up[e].data_ptr(), qt, I, H, yu.data_ptr(), stream))
+                _check(L.moe_gguf_matmul_t(a.data_ptr(), B, down[e].data_ptr(), qt, H, I, yd.data_ptr(), stream))
+            ms = _time_calls(expert, 128)
+            byts = ebytes + B * (2 * H + 3 * I) * 4 + B * (2 * I + H) * 4
+            flops = 2.0 * B * 3 * H * I
+            res[f"{name}_B{B}"] = dict(us_per_expert=round(ms * 1e3, 2), gbs=round(byts / ms / 1e6, 1),
+                                       hbm_frac=round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                       fp32_frac=round(flops / ms / 1e9 / FP32_PEAK_TFLOPS, 4),
+                                       bytes_per_expert=ebytes)
+            log(f"gguf {name} B={B}: {ms * 1e3:.1f} us/expert, {byts / ms / 1e6:.0f} GB/s")
+            del x, a, yg, yu, yd
+        del gate, up, down
+    res["workload"] = ("C3: GGUF Q8_0 / Q4_K experts, gate and up [768 x 2048], down [2048 x 768], three "
+                       "gguf_matmul_t calls per expert evaluation, B routed rows, pools of 128 (Q8_0, 642 MB) and "
+                       "256 (Q4_K, 680 MB) experts")
+    torch.cuda.empty_cache()
+    return res
+
+
 def wire_codec(args, L, n: int = 8192, d: int = 4096):
     """Wire encode (moe_wire_encode) of an [n, d] f32 block in HBM (128 MB) to
     int8 + scales and to f16, and the int8 decode back: bytes read + written
@@ -428,15 +570,37 @@ def cpu_baseline_decode(seconds: float = 12.0):
         L.ref_moe_q4(x.ctypes.data, 1, pt.ctypes.data, xors.ctypes.data, poff.ctypes.data, prow.ctypes.data,
                      pw.ctypes.data, per_call, per_call, H, I, gs, out.ctypes.data)
     call(0)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        call(n + 1)
-        n += 1
-    dt = time.perf_counter() - t0
-    byts = n * per_call * expert_bytes(H, I, gs)
-    return dict(value=byts / dt / 1e9, unit="GB/s", cores=int(L.ref_threads()), kind="port",
-                sample=f"{n} calls x 384 experts (one token, H=2048 I=768 gs=32) from a 64-expert host pool, "
-                       f"{dt:.1f} s; oracle/cpuref.c ref_moe_q4 (the _moe_q4 loop structure), OpenMP")
+    rounds, total_calls = [], 0
+    for _ in range(3):   # median of 3 rounds, as the reference's bench_expert (moelan/experts.py:366-373)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 3:
+            call(total_calls + n + 1)
+            n += 1
+        dt = time.perf_counter() - t0
+        total_calls += n
+        rounds.append(n * per_call * expert_bytes(H, I, gs) / dt / 1e9)
+    value = float(np.median(rounds))
+    return dict(value=value, unit="GB/s", cores=int(L.ref_threads()), kind="port",
+                rounds_gbs=[round(r, 2) for r in rounds], host=host_info(),
+                sample=f"median of 3 rounds of ~{seconds / 3:.0f} s ({total_calls} calls in all) of one token's 384 "
+                       f"experts (H=2048 I=768 gs=32) from a 64-expert host pool (170 MB); oracle/cpuref.c "
+                       f"ref_moe_q4 (the _moe_q4 loop structure), OpenMP over {int(L.ref_threads())} threads")
+
+
+def host_info() -> dict:
+    """The host the CPU baseline ran on: CPU model, the cores this process may
+    run on, and the thread settings OpenMP / BLAS read."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(cpu_model=model, affinity_cores=len(os.sched_getaffinity(0)),
+                OMP_NUM_THREADS=os.environ.get("OMP_NUM_THREADS"),
+                OPENBLAS_NUM_THREADS=os.environ.get("OPENBLAS_NUM_THREADS"))
 
 
 def zipf_calls(rng, B: int, E: int = 128, k: int = 8, s: float = 1.1):
@@ -622,6 +786,7 @@ def cpu_baseline_prefill(seconds: float = 6.0):
     layer_s = per_expert * 128
     return dict(tokens_per_s=512 / layer_s, layer_ms=layer_s * 1e3, experts_timed=n,
                 threads=os.environ.get("OMP_NUM_THREADS") or str(len(os.sched_getaffinity(0))),
+                host=host_info(),
                 kind="port", sample=f"{n} experts x 32 rows: numpy widen (oracle q4_dequant) + BLAS x @ W.T, "
                                     f"scaled to a 128-expert layer")
 
@@ -631,7 +796,6 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--stack", action="store_true", help="also run the 235B-shaped resident stack decode")
     ap.add_argument("--extras", action="store_true",
                     help="also run the group-64 int8/float decode, GGUF, wire and residency measurements "
                          "(each has its own --only part; kept out of the default run so that the default "
@@ -671,6 +835,10 @@ def main() -> int:
             res["wire"] = wire_codec(args, L)
         if "residency" in only:
             res["residency"] = residency(args, L)
+        if "int8" in only:
+            res["int8_c2"] = int8_c2(args, L)
+        if "gguf_c3" in only:
+            res["gguf_c3"] = gguf_c3(args, L)
         if "stack" in only:
             res["stack"] = stack_decode(args, L, tuple(int(b) for b in args.batches.split(",")))
         if "copy" in only:   # a plain device copy of known size (calibrates the traffic counters)
@@ -697,8 +865,12 @@ def main() -> int:
         extras["gguf_matvec"] = gguf_matvec(args, L)
         extras["wire"] = wire_codec(args, L)
         extras["residency"] = residency(args, L)
-    if args.stack:
-        extras["stack_235b"] = stack_decode(args, L)
+    log("C5: Qwen3-235B-A22B-shaped stack decode ...")
+    extras["stack_235b"] = stack_decode(args, L, tuple(int(b) for b in args.batches.split(",")))
+    log("C2: int8 experts ...")
+    extras["int8_c2"] = int8_c2(args, L)
+    log("C3: GGUF experts ...")
+    extras["gguf_c3"] = gguf_c3(args, L)
     log("prefill (Qwen3-30B-A3B layer, T=512) ...")
     pf = prefill_c4(args, L)
     log(f"prefill: {pf['ms_per_layer'] * 1e3:.1f} us/layer, {pf['tokens_per_s'] / 1e6:.2f} M tok/s, "
@@ -724,8 +896,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 x f32 (gate|up: i4 dot8 on 23-bit fixed-point activation limbs, i32 accumulate; "
-                 "down: f32 FMA)",
+        "dtype": "int4 weights x f32 activations (both mat-vec launches: i4 dot8 of the nibbles with exact "
+                 "23-bit fixed-point activation limbs per 32/16-value run, i32 sums, f32 group scales and "
+                 "accumulation)",
         "data": "synthetic (seeded uniform nibbles, |N(0,0.02)|/8 f16 scales, N(0,1) activations)",
         "config": {"workload": "int4 expert decode mat-vec: one token's 384 routed-expert evaluations "
                                "(48 layers x top-8) per fused call, Qwen3-30B-A3B expert shape H=2048 I=768, "
