@@ -16,11 +16,55 @@ import numpy as np
 
 from . import kernels
 
-FORMATS = ("int8", "int4", "native")   # resident formats (moelan/experts.py: FORMATS)
+FORMATS = ("f32", "int8", "int4", "native")   # resident formats (moelan/experts.py:40)
 
 
 def _dev_or_none(a):
     return a if kernels.is_device(a) else None
+
+
+def default_threads() -> int:
+    """Loader threads of a store when none are given (moelan/experts.py:50-51)."""
+    import os
+    return max(1, min(8, (os.cpu_count() or 2) // 2))
+
+
+class F32Matrix:
+    """A full-precision (rows, cols) weight (moelan/experts.py:72-89). Its
+    product is a library f32 GEMM on one device copy, made on first use."""
+
+    __slots__ = ("w", "_dev")
+
+    def __init__(self, w):
+        self.w = w if kernels.is_device(w) else np.ascontiguousarray(w, dtype=np.float32)
+        self._dev = None
+
+    def device_arrays(self):
+        if self._dev is None:
+            import torch
+            self._dev = (kernels.to_device(self.w, torch.float32),)
+        return self._dev
+
+    def host_arrays(self):
+        """The host array device_arrays() uploads, with its device shape."""
+        return [(self.w, tuple(self.w.shape))]
+
+    @property
+    def shape(self):
+        return tuple(self.w.shape)
+
+    def matmul_t(self, x):
+        import torch
+        (w,) = self.device_arrays()
+        y = torch.matmul(kernels.to_device(x, torch.float32), w.t())
+        return kernels._ret(y, x)
+
+    def dequant(self):
+        return self.w
+
+    @property
+    def nbytes(self):
+        return int(self.w.nbytes) if not kernels.is_device(self.w) else self.w.numel() * 4
 
 
 class GroupQuant:
@@ -311,14 +355,20 @@ def _copy_pool():
     return _POOL
 
 
-def to_format(e: Expert, fmt: str) -> Expert:
+def to_format(e: Expert, fmt: str, gs: int = 64) -> Expert:
     """An expert in a resident format (moelan/experts.py:276-301): ``native``
     keeps the file's encoding; ``int4`` keeps colibri's bytes as they are (the
-    kernels read them with their XOR); ``int8`` widens int4 nibbles to int8."""
+    kernels read them with their XOR); ``int8`` widens int4 nibbles to int8
+    and rounds f32 matrices to int8 in groups of ``gs``; ``f32`` widens any
+    matrix to full precision (on the device)."""
     if fmt == "native":
         return e
+    if fmt not in FORMATS:
+        raise ValueError(f"unknown expert format {fmt!r}")
 
     def conv(m):
+        if fmt == "f32":
+            return m if isinstance(m, F32Matrix) else F32Matrix(m.dequant())
         if fmt == "int4":
             if isinstance(m, Packed4):
                 return m
@@ -327,6 +377,9 @@ def to_format(e: Expert, fmt: str) -> Expert:
             return m.to_int8()
         if isinstance(m, GroupQuant):
             return m
+        if isinstance(m, F32Matrix):
+            w = m.w.cpu().numpy() if kernels.is_device(m.w) else m.w
+            return GroupQuant.quantize(w, gs)
         raise ValueError(f"int8 residency of a {type(m).__name__} matrix is not provided")
     return Expert(conv(e.gu), conv(e.down), e.inter)
 
@@ -344,14 +397,19 @@ class ExpertStore:
       copy it made on first use while it is listed.
     Hits count pinned and LRU experts, misses the others (as the reference).
     ``sources`` may also be a dict {(layer, expert): Expert} of experts to pin.
+    The arguments are the reference's (moelan/experts.py:538-540): ``threads``
+    read experts out of their sources in parallel in :meth:`pin`, ``gs`` is the
+    group of the int8 format's rounding of f32 matrices.
     """
 
-    def __init__(self, sources=None, fmt: str = "int4", lru_size: int = 0, map_size: int = 4096):
+    def __init__(self, sources=None, fmt: str = "int4", lru_size: int = 0, threads: int | None = None,
+                 gs: int = 64, map_size: int = 4096):
         from collections import OrderedDict
         if fmt not in FORMATS:
             raise ValueError(f"format must be one of {FORMATS}")
-        self.fmt = fmt
+        self.fmt, self.gs = fmt, gs
         self.lru_size, self.map_size = lru_size, map_size
+        self.threads = threads or default_threads()
         self.pinned: dict = {}
         self.lru: OrderedDict = OrderedDict()
         self.mapped: OrderedDict = OrderedDict()
@@ -367,7 +425,7 @@ class ExpertStore:
         for src in self.sources:
             if src.has(key):
                 e = src.load(key)
-                return (to_format(e, fmt) if fmt else e), src
+                return (to_format(e, fmt, self.gs) if fmt else e), src
         raise KeyError(f"expert {key} is not available on this node")
 
     def can_serve(self, key) -> bool:
@@ -376,19 +434,27 @@ class ExpertStore:
 
     def pin(self, items) -> None:
         """Pin experts and upload their arrays now: keys (read from the
-        sources, moelan/experts.py:581-590) or ((layer, expert), Expert) pairs."""
-        new = []
+        sources, ``threads`` at a time, moelan/experts.py:581-590) or
+        ((layer, expert), Expert) pairs."""
+        given, keys = [], []
         for it in items:
             if len(it) == 2 and isinstance(it[1], Expert):
-                key, e = tuple(it[0]), it[1]
-            else:
-                key = tuple(it)
-                if key in self.pinned:
-                    continue
-                e = self.lru.pop(key, None) or self.mapped.pop(key, None) or self._read_from(key, self.fmt)[0]
+                given.append((tuple(it[0]), it[1]))
+            elif tuple(it) not in self.pinned and tuple(it) not in keys:
+                keys.append(tuple(it))
+
+        def read(key):
+            e = self.lru.pop(key, None) or self.mapped.pop(key, None)
+            return key, (to_format(e, self.fmt, self.gs) if e is not None else self._read_from(key, self.fmt)[0])
+        if self.threads > 1 and len(keys) > 1:
+            from concurrent.futures import ThreadPoolExecutor
+            with ThreadPoolExecutor(min(self.threads, len(keys)), thread_name_prefix="moehip-read") as pool:
+                loaded = list(pool.map(read, keys))
+        else:
+            loaded = [read(k) for k in keys]
+        for key, e in given + loaded:
             self.pinned[key] = e
-            new.append(e)
-        upload_experts(new)
+        upload_experts([e for _, e in given + loaded])
 
     def unpin_all_except(self, keep) -> None:
         keep = {tuple(k) for k in keep}

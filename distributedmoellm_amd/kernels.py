@@ -247,19 +247,96 @@ def int8_act_for(H: int, I: int, gs: int) -> bool:
     return INT8_ACT and gs % 64 == 0 and gs <= 512 and H % gs == 0 and I % gs == 0
 
 
+class HostCopies:
+    """Device copies of host arrays that callers hand over again and again:
+    the int4 matrices of moelan's own store, numpy views of a memory map with
+    no device side of their own. A copy is keyed by the array's address,
+    size, dtype and shape, and lives while some host array with that key
+    does (weak references), so a view made again of the same mapped bytes
+    finds the copy instead of uploading it again, and memory the host frees
+    takes its copy with it. The host arrays are taken as fixed once handed
+    over (moelan's are read-only maps or load-time copies)."""
+
+    def __init__(self):
+        import threading
+        self._lock = threading.RLock()
+        self._copies: dict = {}     # key -> [device tensor, live host arrays]
+        self._watch: dict = {}      # id(host array) -> (weakref, key)
+        self.uploads = 0            # arrays copied to the device so far
+        self.upload_bytes = 0
+
+    def get(self, a, dtype=None):
+        """The device copy of host array ``a`` (made now if there is none)."""
+        import weakref
+        a = a if isinstance(a, np.ndarray) else np.asarray(a)
+        key = (a.__array_interface__["data"][0], a.nbytes, a.dtype.str, a.shape)
+        with self._lock:
+            ent = self._copies.get(key)
+            if ent is None:
+                ent = self._copies[key] = [to_device(a, dtype), 0]
+                self.uploads += 1
+                self.upload_bytes += a.nbytes
+            w = self._watch.get(id(a))
+            if w is None or w[0]() is not a:
+                self._watch[id(a)] = (weakref.ref(a, lambda r, i=id(a): self._gone(i, r)), key)
+                ent[1] += 1
+            # a weak-reference callback run meanwhile (garbage collection in
+            # this thread) may have dropped the entry while ``a`` lives on
+            self._copies[key] = ent
+            return ent[0]
+
+    def _gone(self, ident, ref) -> None:
+        with self._lock:
+            w = self._watch.get(ident)
+            if w is None or w[0] is not ref:
+                return
+            del self._watch[ident]
+            ent = self._copies.get(w[1])
+            if ent is not None:
+                ent[1] -= 1
+                if ent[1] <= 0:
+                    del self._copies[w[1]]
+
+    def __len__(self) -> int:
+        return len(self._copies)
+
+    def nbytes(self) -> int:
+        with self._lock:
+            return sum(t.numel() * t.element_size() for t, _ in self._copies.values())
+
+
+HOST_COPIES = HostCopies()
+
+
+def _q4_arrays(m):
+    """(raw uint8 [O, I/2], scales [O, I/gs]) of an int4 matrix on the device:
+    its own device arrays, or for a matrix with host arrays only (moelan's
+    Packed4: ``raw``, ``s``, ``gs``, ``shape``, ``offset``) the host copy cache's."""
+    if hasattr(m, "device_arrays"):
+        return m.device_arrays()
+    O, I = m.shape
+    raw, s = np.asarray(m.raw), np.asarray(m.s)
+    if raw.dtype != np.uint8 or raw.size != O * I // 2 or s.size != O * (I // m.gs) or \
+            s.dtype not in (np.float32, np.float16):
+        return None
+    return HOST_COPIES.get(raw).reshape(O, I // 2), HOST_COPIES.get(s).reshape(O, I // m.gs)
+
+
 def q4_expert_ptrs(e):
     """What :func:`moe_q4` needs of one int4 expert: the device addresses of its
     four arrays, the XOR for its nibbles and whether its scales are f16; None if
-    it does not qualify (moelan/kernels.py:929-939)."""
+    it does not qualify (moelan/kernels.py:929-939). Experts whose matrices
+    hold host arrays only get device copies from :data:`HOST_COPIES`, made
+    once per host array."""
     gu, dn = e.gu, e.down
-    if not (hasattr(gu, "device_arrays") and hasattr(dn, "device_arrays")):
+    if not all(hasattr(m, a) for m in (gu, dn) for a in ("raw", "s", "gs", "shape", "offset")):
         return None
     if gu.gs != dn.gs or gu.offset != dn.offset:
         return None
-    gr, gsc = gu.device_arrays()
-    dr, dsc = dn.device_arrays()
-    if gsc.dtype != dsc.dtype:
+    ga, da = _q4_arrays(gu), _q4_arrays(dn)
+    if ga is None or da is None or ga[1].dtype != da[1].dtype:
         return None
+    (gr, gsc), (dr, dsc) = ga, da
     return (gr.data_ptr(), gsc.data_ptr(), dr.data_ptr(), dsc.data_ptr(), 0 if gu.offset else 0x88,
             1 if gsc.dtype == torch.float16 else 0)
 

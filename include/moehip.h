@@ -145,16 +145,19 @@ int moe_q4_layer(const float* x, int ldx, const moe_q4_expert* table, const int*
                  float* out, int ldo, int H, int I, int gs, int max_rows, void* workspace, size_t ws_bytes,
                  void* stream);
 
-/* moe_q4_layer with no workspace argument: the call's scratch (the gate|up
- * outputs h [P, 2I] and the down outputs y [P, H], f32) lives in 32 MiB of
- * device memory the library holds on each device it runs on, from the first
- * call there until the process ends, so the call allocates nothing. It has no
- * counterpart in the reference: it is for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). Limit: P * (2I + H) * 4 bytes <= 32 MiB (e.g. 2340 pairs
- * at H=2048, I=768), else MOE_EWORKSPACE. Every call on one device shares
- * that device's scratch: calls that overlap on a device (other streams,
- * other threads) race. Same arguments, results and numerics as moe_q4_layer. */
+/* moe_q4_layer with no workspace argument: the call's scratch (what
+ * moe_q4_layer would take from its workspace: the gate|up outputs h [P, 2I] and
+ * down outputs y [P, H], f32, and for experts with several rows their
+ * activation limbs) lives in 32 MiB of device memory the library holds on
+ * each device it runs on, from the first call there until the process ends,
+ * so the call allocates nothing. It has no counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Limit:
+ * moe_q4_layer_workspace(P, H, I) <= 32 MiB (about 59 KB a pair at H=2048,
+ * I=768: 564 pairs; about 119 KB at H=4096, I=1536: 282 pairs), else
+ * MOE_EWORKSPACE. Every call on one device shares that device's scratch:
+ * calls that overlap on a device (other streams, other threads) race. Same
+ * arguments, results and numerics as moe_q4_layer. */
 int moe_q4_layer_noalloc(const float* x, int ldx, const moe_q4_expert* table, const int* eidx, int k,
                          const int* poff, const int* prow, const float* pw, int P, const int* rrow, const int* rptr,
                          const int* rpair, int nr, float* out, int ldo, int H, int I, int gs, int max_rows,

@@ -64,7 +64,13 @@ def write_gguf(path, meta: dict, tensors: dict, align: int = 32):
     kv = b""
     for k, v in meta.items():
         kv += _gguf_string(k)
-        if isinstance(v, str):
+        if isinstance(v, list) and v and isinstance(v[0], str):
+            kv += struct.pack("<IIQ", 9, 8, len(v)) + b"".join(_gguf_string(t) for t in v)
+        elif isinstance(v, list):
+            kv += struct.pack("<IIQ", 9, 5, len(v)) + struct.pack(f"<{len(v)}i", *v)
+        elif isinstance(v, bool):
+            kv += struct.pack("<I?", 7, v)
+        elif isinstance(v, str):
             kv += struct.pack("<I", 8) + _gguf_string(v)
         elif isinstance(v, float):
             kv += struct.pack("<I", 6) + struct.pack("<f", v)
@@ -237,3 +243,136 @@ def test_store_pinned_experts_and_unpinning():
     assert list(st.pinned) == [(0, 2)] and not st.can_serve((0, 1))
     with pytest.raises(ValueError, match="int4 residency"):
         X.to_format(X.synthetic_expert(64, 32, "int8", 32, rng), "int4")
+
+
+# ---------------------------------------------------------------- format edge cases
+
+def test_safetensors_header_is_checked_against_the_file(tmp_path):
+    p = tmp_path / "a.safetensors"
+    safetensors_numpy.save_file({"x": np.arange(6, dtype=np.float32).reshape(2, 3),
+                                 "b": np.array([1, 2], np.uint16).view(np.uint16)}, str(p))
+    f = S.SafetensorsFile(p)
+    assert np.array_equal(f.get("x"), np.arange(6, dtype=np.float32).reshape(2, 3))
+    view, tag, shape = f.raw("x")
+    assert tag == "F32" and shape == [2, 3] and view.nbytes == 24 and not view.flags.writeable
+    data = p.read_bytes()
+    (tmp_path / "short.safetensors").write_bytes(data[:-8])          # the last tensor cut short
+    with pytest.raises(ValueError, match="past the end"):
+        S.SafetensorsFile(tmp_path / "short.safetensors")
+    hlen = int.from_bytes(data[:8], "little")
+    (tmp_path / "long.safetensors").write_bytes((10 ** 9).to_bytes(8, "little") + data[8:])
+    with pytest.raises(ValueError, match="header length"):
+        S.SafetensorsFile(tmp_path / "long.safetensors")
+    doc = json.loads(data[8:8 + hlen])
+    doc["x"]["shape"] = [2, 4]                                       # 24 bytes cannot hold 2x4 f32
+    head = json.dumps(doc).encode()
+    (tmp_path / "shape.safetensors").write_bytes(len(head).to_bytes(8, "little") + head + data[8 + hlen:])
+    with pytest.raises(ValueError, match="bytes for F32"):
+        S.SafetensorsFile(tmp_path / "shape.safetensors")
+
+
+def test_bf16_tensors_widen_exactly(tmp_path):
+    v = np.array([1.0, -2.5, 3.140625, 1e-3], np.float32)
+    bits = (v.view(np.uint32) >> 16).astype(np.uint16)
+    p = tmp_path / "h.safetensors"
+    head = json.dumps({"t": {"dtype": "BF16", "shape": [4], "data_offsets": [0, 8]}}).encode()
+    p.write_bytes(len(head).to_bytes(8, "little") + head + bits.tobytes())
+    got = S.SafetensorsFile(p).get("t")
+    assert np.array_equal(got, (bits.astype(np.uint32) << 16).view(np.float32))
+
+
+def test_gguf_metadata_values_and_layout_checks(tmp_path):
+    path = tmp_path / "m.gguf"
+    meta = {"general.architecture": "qwen3moe", "tokenizer.ggml.tokens": ["a", "bc", "<|im_end|>"],
+            "qwen3moe.rope.dims": [1, -2, 3], "qwen3moe.flag": True, "qwen3moe.eps": 0.5}
+    write_gguf(path, meta, {"w": (8, (2, 64), np.zeros((2, 68), np.uint8))})
+    g = S.GGUFFile(path)
+    assert g.meta["tokenizer.ggml.tokens"] == ["a", "bc", "<|im_end|>"]
+    assert g.meta["qwen3moe.rope.dims"].tolist() == [1, -2, 3] and g.meta["qwen3moe.flag"] is True
+    assert g.meta["qwen3moe.eps"] == 0.5 and g.data_start % 32 == 0
+    data = bytearray(path.read_bytes())
+    big = bytearray(data)
+    big[4:8] = (3).to_bytes(4, "big")
+    (tmp_path / "be.gguf").write_bytes(bytes(big))
+    with pytest.raises(ValueError, match="big-endian"):
+        S.GGUFFile(tmp_path / "be.gguf")
+    (tmp_path / "cut.gguf").write_bytes(bytes(data[:40]))            # inside the key/value records
+    with pytest.raises(ValueError, match="truncated"):
+        S.GGUFFile(tmp_path / "cut.gguf")
+    odd = tmp_path / "odd.gguf"                                      # a tensor offset off the alignment
+    write_gguf(odd, {"general.architecture": "qwen3moe"}, {"a": (8, (1, 32), np.zeros(34, np.uint8)),
+                                                           "b": (8, (1, 32), np.zeros(34, np.uint8))}, align=2)
+    with pytest.raises(ValueError, match="not aligned"):
+        S.GGUFFile(odd)
+
+
+def test_float_checkpoint_gives_f32_experts(tmp_path):
+    """A Hugging Face checkpoint's float experts (Mixtral naming) load as f32
+    experts: gate and up stacked, exact bf16 widening."""
+    H, I, E = 64, 32, 2
+    rng = np.random.default_rng(7)
+    (tmp_path / "config.json").write_text(json.dumps({"model_type": "mixtral", "hidden_size": H,
+                                                      "intermediate_size": I, "num_local_experts": E,
+                                                      "num_hidden_layers": 1, "num_experts_per_tok": 2}))
+    t, want = {}, {}
+    for e in range(E):
+        p = f"model.layers.0.block_sparse_moe.experts.{e}"
+        g, u, d = (rng.standard_normal(s).astype(np.float32) for s in ((I, H), (I, H), (H, I)))
+        t.update({f"{p}.w1.weight": g, f"{p}.w3.weight": u, f"{p}.w2.weight": d})
+        want[e] = (g, u, d)
+    safetensors_numpy.save_file(t, str(tmp_path / "model.safetensors"))
+    src = S.open_source(tmp_path)
+    assert not src.zero_copy and src.cfg.family == "mixtral" and src.cfg.top_k == 2 and src.has((0, 1))
+    e = src.load((0, 1))
+    g, u, d = want[1]
+    assert isinstance(e.gu, X.F32Matrix) and np.array_equal(e.gu.w, np.concatenate([g, u])) and \
+        np.array_equal(e.down.w, d) and e.inter == I
+
+
+def test_sources_take_a_moelan_style_config(tmp_path):
+    """open_source(model_dir, cfg) with a config object of moelan's fields."""
+    write_colibri(tmp_path / "c", H=256, I=128, gs=64)
+
+    class ModelConfig:                     # the fields moelan/config.py's ModelConfig gives the sources
+        hidden_size, moe_intermediate_size, num_experts = 256, 128, 4
+        expert_layout, expert_gs = "colibri_int4", 64
+
+        def expert_names(self, layer, expert):
+            p = f"model.layers.{layer}.mlp.experts.{expert}"
+            return f"{p}.merged_weight", f"{p}.qs"
+    src = S.open_source(tmp_path / "c", ModelConfig())
+    assert isinstance(src, S.CheckpointSource) and src.zero_copy
+    e = src.load((1, 2))
+    assert e.gu.shape == (256, 256) and e.down.shape == (256, 128)
+    gpath = tmp_path / "m.gguf"
+    gguf_moe(gpath)
+    cfg = S.gguf_config(gpath)
+    assert isinstance(S.open_source(gpath, cfg), S.GGUFSource)
+
+
+def test_store_takes_the_reference_arguments():
+    """ExpertStore(sources, fmt, lru_size, threads, gs, map_size) as moelan's
+    callers pass them; fmt "f32" keeps f32 experts, int8 rounds them in
+    groups of gs."""
+    rng = np.random.default_rng(8)
+    w_gu = rng.standard_normal((64, 64)).astype(np.float32)
+    w_dn = rng.standard_normal((64, 32)).astype(np.float32)
+
+    class F32Source:
+        zero_copy = False
+
+        def has(self, key):
+            return key[0] == 0
+
+        def load(self, key):
+            return X.Expert(X.F32Matrix(w_gu), X.F32Matrix(w_dn), 32)
+    st = X.ExpertStore([F32Source()], fmt="f32", lru_size=4, threads=3, gs=32, map_size=8)
+    assert st.threads == 3 and st.gs == 32 and st.fmt == "f32"
+    e, _ = st._read_from((0, 2), st.fmt)                  # what pin() holds (the upload needs a GPU)
+    assert isinstance(e.gu, X.F32Matrix)
+    st8 = X.ExpertStore([F32Source()], fmt="int8", gs=32)
+    q = st8._read_from((0, 0), st8.fmt)[0].gu
+    assert isinstance(q, X.GroupQuant) and q.gs == 32 and q.s.shape == (64, 2)
+    assert np.abs(q.q.astype(np.float32) * np.repeat(q.s, 32, axis=1) - w_gu).max() <= q.s.max() / 2 + 1e-6
+    with pytest.raises(ValueError, match="format"):
+        X.ExpertStore([], fmt="bf16")
