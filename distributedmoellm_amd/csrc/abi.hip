@@ -422,7 +422,9 @@ struct PrefillWs {
   int* offsets;
   int* n_used;
   _Float16* xs;
+  float* xf;
   _Float16* act;
+  float* af;
   float* y;
   size_t bytes;
 };
@@ -447,28 +449,26 @@ static PrefillWs prefill_layout(void* base, int T, int E, int k, int H, int I) {
   w.offsets = (int*)take(((size_t)E + 1) * 4);
   w.n_used = (int*)take(4);
   w.xs = (_Float16*)take(P * H * 2);
+  w.xf = (float*)take(P * 4);
   w.act = (_Float16*)take(P * I * 2);
+  w.af = (float*)take(P * (I / 16) * 4);
   w.y = (float*)take(P * H * 4);
   w.bytes = off;
   return w;
 }
 
-// xs: [P, H] f16 scratch for the gathered rows (null: the gate|up product reads
-// the f32 rows through `rows` itself)
+// The expert FFN of grouped rows on the MFMA GEMM: xs / xf take the gathered
+// f16 rows and their factors, act / af silu(gate) * up and its factors (per row
+// and 16 columns); y [P, H] f32.
 static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nexp, const int* eoff, const int* rows,
-                       int P, int H, int I, int gs, _Float16* xs, _Float16* act, float* y, int ldy, hipStream_t st) {
+                       int P, int H, int I, int gs, _Float16* xs, float* xf, _Float16* act, float* af, float* y,
+                       int ldy, hipStream_t st) {
+  int rc = run_gather_f16(x, ldx, rows, P, H, xs, xf, st);
+  if (rc) return rc;
   GemmArgs g{};
-  if (xs) {
-    int rc = run_gather_f16(x, ldx, rows, P, H, xs, st);
-    if (rc) return rc;
-    g.A = xs;
-    g.lda = H;
-  } else {
-    g.rows32 = 1;
-    g.X = x;
-    g.ldx = ldx;
-    g.rows = rows;
-  }
+  g.A = xs;
+  g.lda = H;
+  g.xfac = xf;
   g.eoff = eoff;
   g.table = table;
   g.which = 0;
@@ -477,11 +477,15 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   g.gs = gs;
   g.act = act;
   g.ldact = I;
-  int rc = run_gemm(MODE_GATE_UP, g, nexp, st);
+  g.act_fac = af;
+  g.ldaf_out = I / 16;
+  rc = run_gemm(MODE_GATE_UP, g, nexp, st);
   if (rc) return rc;
   GemmArgs d{};
   d.A = act;
   d.lda = I;
+  d.afac = af;
+  d.ldaf = I / 16;
   d.eoff = eoff;
   d.table = table;
   d.which = 1;
@@ -541,9 +545,20 @@ MOE_API int moe_group_by_expert(const int* idx, const float* w, int T, int k, in
   return run_group(idx, w, T, k, E, eoff, rows, wts, pos, experts, offsets, n_used, as_stream(stream));
 }
 
+// the grouped FFN's scratch: gathered rows, their factors, silu(gate) * up and its factors
+static size_t ffn_parts(int P, int H, int I, size_t* at) {
+  const size_t n[4] = {(size_t)P * H * 2, (size_t)P * 4, (size_t)P * I * 2, (size_t)P * (I / 16) * 4};
+  size_t off = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (at) at[i] = off;
+    off += align256(n[i]);
+  }
+  return off;
+}
+
 MOE_API size_t moe_q4_grouped_ffn_workspace(int P, int H, int I) {
   if (P <= 0 || H <= 0 || I <= 0) return 0;
-  return align256((size_t)P * H * 2) + align256((size_t)P * I * 2);
+  return ffn_parts(P, H, I, nullptr);
 }
 
 MOE_API int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* table, int nexp, const int* eoff,
@@ -559,10 +574,12 @@ MOE_API int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* tab
   if (!workspace || ws_bytes < need)
     return set_error(MOE_EWORKSPACE, "moe_q4_grouped_ffn: workspace of %zu bytes, %zu needed", ws_bytes, need);
   REQUIRE(aligned(workspace, 256), "moe_q4_grouped_ffn: workspace must be 256-byte aligned");
-  _Float16* xs = (_Float16*)workspace;
-  _Float16* act = (_Float16*)((char*)workspace + align256((size_t)P * H * 2));
-  return grouped_ffn(x, ldx, reinterpret_cast<const ExpertDesc*>(table), nexp, eoff, rows, P, H, I, gs, xs, act, y,
-                     ldy, as_stream(stream));
+  size_t at[4];
+  ffn_parts(P, H, I, at);
+  char* b = (char*)workspace;
+  return grouped_ffn(x, ldx, reinterpret_cast<const ExpertDesc*>(table), nexp, eoff, rows, P, H, I, gs,
+                     (_Float16*)(b + at[0]), (float*)(b + at[1]), (_Float16*)(b + at[2]), (float*)(b + at[3]), y, ldy,
+                     as_stream(stream));
 }
 
 MOE_API size_t moe_prefill_workspace(int T, int E, int k, int H, int I) {
@@ -601,7 +618,8 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
     }
     if (!rc) rc = run_route(w.logits, nz, n, E, k, normalize, w.idx, w.w, st);
     if (!rc) rc = run_group(w.idx, w.w, n, k, E, w.eoff, w.rows, w.wts, w.pos, nullptr, nullptr, nullptr, st);
-    if (!rc) rc = grouped_ffn(xp, ldx, tab, E, w.eoff, w.rows, n * k, H, I, gs, w.xs, w.act, w.y, H, st);
+    if (!rc)
+      rc = grouped_ffn(xp, ldx, tab, E, w.eoff, w.rows, n * k, H, I, gs, w.xs, w.xf, w.act, w.af, w.y, H, st);
     if (!rc) rc = run_token_combine(w.y, H, w.pos, w.wts, n, k, H, out + (size_t)t0 * ldo, ldo, st);
     if (rc) return rc;
   }

@@ -7,9 +7,16 @@ namespace moe {
 enum { MODE_PLAIN = 0, MODE_GATE_UP = 1, MODE_DOWN = 2 };
 
 struct GemmArgs {
-  const _Float16* A;  // [P, K] activations, f16, 8-column groups in MFMA order (rows32 == 0)
+  // Activations: f16 rows (8-column groups in MFMA order), each row scaled by
+  // a power of two (GATE_UP: xfac[m] undoes it; DOWN: afac[m * ldaf + c]
+  // undoes it for 16-column piece c), or
+  // f32 rows X (PLAIN, rows32) scaled per row while staged.
+  const _Float16* A;  // [P, K] (rows32 == 0)
   int lda;
-  int rows32;          // activations are f32 rows of X gathered through `rows`
+  const float* xfac;  // GATE_UP
+  const float* afac;  // DOWN
+  int ldaf;
+  int rows32;          // activations are f32 rows of X gathered through `rows` (PLAIN only)
   const float* X;      // [*, ldx] f32
   int ldx;
   const int* rows;     // row of X for each grouped row (null: the grouped row itself)
@@ -24,8 +31,10 @@ struct GemmArgs {
   int gs;
   float* Y;  // PLAIN / DOWN output [P, N] f32
   int ldy;
-  _Float16* act;  // GATE_UP output [P, I] f16, MFMA column order
-  int ldact;
+  _Float16* act;  // GATE_UP output silu(gate) * up [P, I] f16, MFMA column order, each row and
+  int ldact;      // 16 columns scaled by a power of two that act_fac[m * ldaf_out + c] undoes
+  float* act_fac;
+  int ldaf_out;
 };
 
 int router_slices(int T, int E, int H);
@@ -44,7 +53,10 @@ int run_route(const float* logits, int nz, int T, int E, int k, int normalize, i
 // experts / offsets / n_used may be null (not produced)
 int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
               int* experts, int* offsets, int* n_used, hipStream_t st);
-int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, hipStream_t st);
+// Xs[q] = f16(x[rows[q]] * 2^a_q) in MFMA column order, a_q putting the row's
+// largest |value| in [2^13, 2^14); fac[q] = 2^-a_q (1 for a row of zeros or
+// with non-finite values)
+int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, float* fac, hipStream_t st);
 int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st);
 int run_token_combine(const float* y, int ldy, const int* pos, const float* wts, int T, int k, int H, float* out,
                       int ldo, hipStream_t st);

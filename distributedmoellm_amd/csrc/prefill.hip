@@ -357,21 +357,61 @@ __global__ __launch_bounds__(1024) void used_experts_kernel(const int* eoff, int
 
 // ------------------------------------------------------------------ gather
 
-// Xs[q, :] = f16(x[rows[q], :]) with each 8 columns in MFMA order.
-__global__ void gather_f16_kernel(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, int ldxs) {
-  const int groups = K / 8;
-  const long total = (long)P * groups;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
-    const int q = (int)(i / groups), g = (int)(i % groups);
-    const float* src = x + (size_t)(rows ? rows[q] : q) * ldx + 8 * g;
-    float v[8];
+// 2^(t - e) for m = f * 2^e, f in [0.5, 1): m times it lands in [2^(t-1), 2^t);
+// 1 for m = 0 or non-finite m
+__device__ __forceinline__ float pow2_into(float m, int t) {
+  if (!(m > 0.f && m < INFINITY)) return 1.f;
+  return ldexpf(1.f, t - __builtin_amdgcn_frexp_expf(m));
+}
+
+// Xs[q, :] = f16(x[rows[q], :] * 2^a) with each 8 columns in MFMA order, the
+// power chosen from the row's largest |value| (so no value overflows f16);
+// fac[q] = 2^-a. One wave a row.
+__global__ __launch_bounds__(256) void gather_f16_kernel(const float* x, int ldx, const int* rows, int P, int K,
+                                                         _Float16* Xs, int ldxs, float* fac) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (q >= P) return;
+  const float* src = x + (size_t)(rows ? rows[q] : q) * ldx;
+  _Float16* dst = Xs + (size_t)q * ldxs;
+  // rows of up to 2048 values stay in registers between the two passes
+  constexpr int kHeld = 4;  // 8-column groups a lane holds
+  float4 held[kHeld][2];
+  float m = 0.f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = src[c];
+  for (int k = 0; k < kHeld; ++k) {
+    const int c = 8 * lane + 512 * k;
+    if (c < K) {
+      held[k][0] = *reinterpret_cast<const float4*>(src + c);
+      held[k][1] = *reinterpret_cast<const float4*>(src + c + 4);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(held[k][h].x), fabsf(held[k][h].y)),
+                           fmaxf(fabsf(held[k][h].z), fabsf(held[k][h].w))));
+    }
+  }
+  for (int c = 8 * lane + 512 * kHeld; c < K; c += 512) {
+    const float4 lo = *reinterpret_cast<const float4*>(src + c), hi = *reinterpret_cast<const float4*>(src + c + 4);
+    m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
+                       fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w)))));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  const float f = pow2_into(m, 14);
+  auto put = [&](int c, float4 lo, float4 hi) {
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     half8 h;
 #pragma unroll
-    for (int p = 0; p < 8; ++p) h[p] = (_Float16)v[(p & 1) * 4 + (p >> 1)];
-    *reinterpret_cast<half8*>(Xs + (size_t)q * ldxs + 8 * g) = h;
+    for (int p = 0; p < 8; ++p) h[p] = (_Float16)(v[(p & 1) * 4 + (p >> 1)] * f);
+    *reinterpret_cast<half8*>(dst + c) = h;
+  };
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {
+    const int c = 8 * lane + 512 * k;
+    if (c < K) put(c, held[k][0], held[k][1]);
   }
+  for (int c = 8 * lane + 512 * kHeld; c < K; c += 512)
+    put(c, *reinterpret_cast<const float4*>(src + c), *reinterpret_cast<const float4*>(src + c + 4));
+  if (lane == 0) fac[q] = 1.f / f;
 }
 
 // ------------------------------------------------------------------ grouped GEMM
@@ -426,16 +466,28 @@ __device__ __forceinline__ half8 widen8(uint32_t w, __half2 s2, uint32_t c0, uin
 // (32 for f32 rows) is done in passes (its weight tile read again).
 // Activations: f16 rows (8-column groups in MFMA order), or f32 rows of X
 // gathered through `rows` and rounded to f16 when staged.
+// Range: every f16 activation is its value times a power of two, undone on
+// the f32 sums in the epilogue, so no activation overflows f16 where f32
+// stays finite:
+//   GATE_UP: per row, chosen by the gather from the row's largest |value|;
+//   DOWN: silu(gate) * up is written per row and 16 columns with the power
+//         that puts the piece's largest |value| in [2^13, 2^14); staging
+//         brings every piece of a row to its largest piece's power;
+//   PLAIN (f32 rows): per row, chosen when the pass starts.
+// Weights are (u - 8) * s rounded once to f16: scales above 8188 overflow and
+// scales below 2^-14 / 8 lose precision (f16 subnormals); int4 group scales
+// are far inside that range.
 
 constexpr int kGK = 128;                   // K per step
-constexpr int kGRows = 64;                 // expert rows per pass
+constexpr int kGRows = 48;                 // expert rows per pass (f16 activations)
 constexpr int kARow = kGK * 2 + 16;        // LDS bytes per activation row (16 B of padding: conflict-free)
 constexpr int kABuf = kGRows * kARow;      // one step's activation tile
 constexpr int kBRow = 128 + 16;            // LDS bytes per weight row of a pair of steps (padded)
 constexpr int kBWave = 32 * kBRow;         // a wave's weight rows
 constexpr int kSRow = 144;                 // LDS bytes per row of a wave's scale window (16-byte aligned)
 constexpr int kSWave = 32 * kSRow;         // a wave's scale rows
-constexpr int kGemmLds = 2 * kABuf + 4 * kBWave + 4 * kSWave;
+constexpr int kFacOff = 2 * kABuf + 4 * kBWave + 4 * kSWave;  // per row of the pass: the factor undoing its scaling
+constexpr int kGemmLds = kFacOff + kGRows * 4;
 
 template <bool SF16>
 __device__ __forceinline__ uint32_t gscale_bits(const void* s, uint32_t i) {
@@ -544,7 +596,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
   const uint32_t c0 = widen_c0(xor4), c1 = widen_c1(xor4);
   const int srow = tid >> 4, aseg = tid & 15;  // staging: row 16 i + srow, 16 bytes at 16 aseg
 
-  // f32 rows take twice the registers per staged row: passes of 32 rows
+  // f32 rows take twice the registers per staged row: passes of 32 rows; f16
+  // rows: passes of 48 (a fourth row tile would not fit the registers beside
+  // the scaling of silu(gate) * up)
   constexpr int kPassRows = ROWS32 ? 32 : kGRows;
   for (int mb = m0; mb < m1; mb += kPassRows) {
     const int rows = min(kPassRows, m1 - mb);
@@ -556,12 +610,69 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
         const int am = mb + min(16 * i + srow, rows - 1);
         arow[i] = ROWS32 ? (a.rows ? a.rows[am] : am) : am;
       }
+      float* const fbuf = reinterpret_cast<float*>(lds + kFacOff);
+      // Each staged row's undoing factor, for the epilogue (row 16 i + srow of
+      // the pass, in LDS), and what staging multiplies by:
+      //   GATE_UP: the gathered row's factor;
+      //   DOWN: silu(gate) * up comes scaled per row and 16 columns (af: its
+      //         undoing factors); staging rescales every piece to the row's
+      //         largest factor (the piece with the largest values), so one
+      //         factor per row remains;
+      //   PLAIN: f32 rows, scaled while staged by the power of two that puts
+      //         the row's largest |value| in [2^13, 2^14) (found here first).
+      // The factors are read before the pipeline's first loads (oldest, so that
+      // waiting for them waits for nothing newer) and committed after them.
+      float rowf[RT];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        rowf[i] = 1.f;
+        if constexpr (MODE == MODE_GATE_UP) {
+          rowf[i] = a.xfac ? a.xfac[arow[i]] : 1.f;
+        } else if constexpr (MODE == MODE_DOWN) {  // the row's factors, 16 threads a row
+          const float* af = a.afac + (size_t)arow[i] * a.ldaf;
+          const int n = a.K / 16;
+          float v[4];  // independent loads, all in flight at once (rows of up to 1024 values)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = aseg + 16 * k < n ? af[aseg + 16 * k] : 0.f;
+          rowf[i] = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+          for (int c = aseg + 64; c < n; c += 16) rowf[i] = fmaxf(rowf[i], af[c]);
+        }
+      }
+      auto stage_factors = [&]() {
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const int r = 16 * i + srow;
+          if constexpr (MODE == MODE_GATE_UP) {
+            if (aseg == 0) fbuf[r] = rowf[i];
+          } else if constexpr (MODE == MODE_DOWN) {
+            // the largest over the row's 16 threads
+            float m = rowf[i];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            m = m > 0.f ? m : 1.f;
+            rowf[i] = m;
+            if (aseg == 0) fbuf[r] = m;
+          } else if constexpr (ROWS32) {
+            const float* xr = a.X + (size_t)arow[i] * a.ldx;
+            float m = 0.f;
+            for (int c = 4 * aseg; c < a.K; c += 64) {
+              const float4 v = *reinterpret_cast<const float4*>(xr + c);
+              m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            rowf[i] = pow2_into(m, 14);
+            if (aseg == 0) fbuf[r] = 1.f / rowf[i];
+          }
+        }
+      };
       // a step's share of the tile: RT x 16 bytes of f16, or RT x 8 floats;
       // two sets, named by compile-time constants only (so that they stay in
       // registers)
       using AVec = std::conditional_t<ROWS32, float4, u32x4>;
       constexpr int kAV = ROWS32 ? 2 * RT : RT;
       AVec areg[2][kAV];
+      float pfac[2][RT];  // DOWN: the undoing factor of the staged piece's 16 columns
       auto load_a = [&](int st, auto set) {
         constexpr int R = decltype(set)::value;
 #pragma unroll
@@ -572,6 +683,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
             areg[R][2 * i + 1] = src[1];
           } else {
             areg[R][i] = *reinterpret_cast<const u32x4*>(a.A + (size_t)arow[i] * a.lda + st * kGK + 8 * aseg);
+            if constexpr (MODE == MODE_DOWN)
+              pfac[R][i] = *gptr<float>(a.afac + (size_t)arow[i] * a.ldaf + 8 * st + (aseg >> 1));
           }
         }
       };
@@ -586,8 +699,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
             const float c[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             half8 h;
 #pragma unroll
-            for (int p = 0; p < 8; ++p) h[p] = (_Float16)c[(p & 1) * 4 + (p >> 1)];
+            for (int p = 0; p < 8; ++p) h[p] = (_Float16)(c[(p & 1) * 4 + (p >> 1)] * rowf[i]);
             *reinterpret_cast<half8*>(dst) = h;
+          } else if constexpr (MODE == MODE_DOWN) {
+            // to the row's scaling: times a power of two at most 1, exact but
+            // where it reaches f16's subnormals
+            const float ratio = pfac[R][i] * __builtin_amdgcn_rcpf(rowf[i]);
+            const half8 v = __builtin_bit_cast(half8, areg[R][i]) * (_Float16)ratio;
+            *reinterpret_cast<half8*>(dst) = v;
           } else {
             *reinterpret_cast<u32x4*>(dst) = areg[R][i];
           }
@@ -679,6 +798,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
       __builtin_amdgcn_sched_barrier(0);
       load_s(min(1, lastp), IC<1>{});
       __builtin_amdgcn_sched_barrier(0);
+      stage_factors();
       int p = 0;
       for (; p + 2 < npairs; p += 2) {
         body(p, IC<0>{}, true);
@@ -692,20 +812,40 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
       }
 
       // D layout: lane (ln, q) holds rows 4q .. 4q+3 of column ln of each 16x16 tile
+      if constexpr (MODE == MODE_GATE_UP) {
+        // silu(gate) * up of the wave's 16 columns, scaled per row by the power
+        // of two that puts their largest |value| in [2^13, 2^14)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = mb + 16 * rt + 4 * q + j;
-          if (m >= m1) continue;
-          if (MODE == MODE_GATE_UP) {
-            if (wok[0])
-              a.act[(size_t)m * a.ldact + perm_pos(nbase + 16 * wave + ln)] =
-                  (_Float16)(silu(acc[rt][0][j]) * acc[rt][1][j]);
-          } else {
+          for (int j = 0; j < 4; ++j) {
+            const int r = 16 * rt + 4 * q + j, m = mb + r;
+            const float fx = fbuf[r];
+            const float av = silu(acc[rt][0][j] * fx) * (acc[rt][1][j] * fx);
+            float mx = wok[0] ? fabsf(av) : 0.f;
+            // every lane of the 16 gets their largest (rotations within the row)
+            mx = fmaxf(mx, dpp_read<0x128, 0xf, false>(mx));  // row_ror:8
+            mx = fmaxf(mx, dpp_read<0x124, 0xf, false>(mx));  // row_ror:4
+            mx = fmaxf(mx, dpp_read<0x4E, 0xf, false>(mx));   // quad_perm [2,3,0,1]
+            mx = fmaxf(mx, dpp_read<0xB1, 0xf, false>(mx));   // quad_perm [1,0,3,2]
+            const float f = pow2_into(mx, 14);
+            if (m < m1) {
+              if (wok[0]) a.act[(size_t)m * a.ldact + perm_pos(nbase + 16 * wave + ln)] = (_Float16)(av * f);
+              if (ln == 0) a.act_fac[(size_t)m * a.ldaf_out + nbase / 16 + wave] = 1.f / f;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int m = mb + 16 * rt + 4 * q + j;
+            if (m >= m1) continue;
+            const float f = fbuf[16 * rt + 4 * q + j];
 #pragma unroll
             for (int s = 0; s < 2; ++s)
-              if (wok[s]) a.Y[(size_t)m * a.ldy + nbase + 32 * wave + 16 * s + ln] = acc[rt][s][j];
+              if (wok[s]) a.Y[(size_t)m * a.ldy + nbase + 32 * wave + 16 * s + ln] = acc[rt][s][j] * f;
           }
         }
       }
@@ -718,8 +858,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
       switch ((rows + 15) >> 4) {
         case 1: pass(IC<1>{}); break;
         case 2: pass(IC<2>{}); break;
-        case 3: pass(IC<3>{}); break;
-        default: pass(IC<4>{}); break;
+        default: pass(IC<3>{}); break;
       }
     }
     __syncthreads();  // the LDS tiles are refilled by the next pass
@@ -889,10 +1028,9 @@ int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, in
   return check_launch("group by expert (used experts)");
 }
 
-int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, hipStream_t st) {
+int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Float16* Xs, float* fac, hipStream_t st) {
   if (P <= 0) return MOE_OK;
-  hipLaunchKernelGGL(gather_f16_kernel, dim3(blocks_for((long)P * K / 8)), dim3(256), 0, st, x, ldx, rows, P, K, Xs,
-                     K);
+  hipLaunchKernelGGL(gather_f16_kernel, dim3((P + 3) / 4), dim3(256), 0, st, x, ldx, rows, P, K, Xs, K, fac);
   return check_launch("gather rows (f16)");
 }
 
@@ -904,8 +1042,7 @@ int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
   auto go = [&](auto k) { hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a); };
   if (a.rows32) {
     if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, true>);
-    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, true>);
-    else return set_error(MOE_EINVAL, "int4 grouped GEMM: the down product takes f16 activations");
+    else return set_error(MOE_EINVAL, "int4 grouped GEMM: only the plain product takes f32 rows");
   } else {
     if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, false>);
     else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, false>);

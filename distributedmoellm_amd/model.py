@@ -1,9 +1,14 @@
-"""Routing and the local expert backend, on the device.
+"""The routed part of a MoE layer, as moelan's model module exposes it.
 
-Mirrors the routed part of ``moelan/model.py``: ``route`` (154-167, softmax
-83-86), ``group_by_expert`` (226-236), ``ExpertBackend`` / ``LocalBackend``
-(243-278), and a layer call that runs all of it on the device for prompts
-(``moe_layer``: router product 597, routing 603, expert call 606).
+moelan's ``model.py`` holds the router's top-k selection (``route``,
+moelan/model.py:154-167, with its softmax 83-86), the grouping of routed rows
+by expert (``group_by_expert``, 226-236) and the expert backends the layers
+call (``ExpertBackend`` / ``LocalBackend``, 243-278). The same names are here
+so that moelan's layer code can import them from this package: the routing
+functions are the device kernels of :mod:`distributedmoellm_amd.kernels`
+under moelan's names, and :func:`moe_layer` runs a prompt's whole MoE layer
+(router product, routing, grouping, expert FFN, weighted sum; moelan/model.py:
+597-606) as one device call.
 """
 
 from __future__ import annotations
@@ -17,17 +22,27 @@ from . import kernels
 
 
 def route(logits, top_k: int, normalize: bool):
-    """Softmax router, top-k selection: (expert ids (n,k) int32, weights (n,k) f32)."""
+    """Top-k experts per row of router logits: (ids (n, k) int32, gate weights
+    (n, k) f32), on the device."""
     return kernels.route(logits, top_k, normalize)
 
 
 def group_by_expert(idx, w, num_experts: int | None = None):
-    """(n,k) routing -> experts, offsets, rows, weights (rows grouped per expert)."""
+    """Routing (n, k) regrouped per expert: (experts, offsets, rows, weights),
+    the rows of expert i being rows[offsets[i]:offsets[i + 1]]."""
     return kernels.group_by_expert(idx, w, num_experts)
 
 
+def _host(a) -> np.ndarray:
+    return a.cpu().numpy() if kernels.is_device(a) else np.asarray(a)
+
+
 class ExpertBackend:
-    """Computes sum_k w_k * expert_k(x) for routed rows. Records routing heat."""
+    """What a MoE layer calls for its routed experts: ``moe(layer, x, idx, w)``
+    returns, per row r of x, the sum over j of w[r, j] times expert idx[r, j]
+    applied to x[r]. Every call also counts how often each (layer, expert) was
+    picked (``heat``), keeps the experts the last row picked (``last``) and
+    adds its wall time to ``moe_time``; subclasses supply ``_moe``."""
 
     def __init__(self):
         self.heat: Counter = Counter()
@@ -35,40 +50,40 @@ class ExpertBackend:
         self.moe_time = 0.0
 
     def moe(self, layer: int, x, idx, w):
-        t0 = time.perf_counter()
-        idx_h = idx.cpu().numpy() if kernels.is_device(idx) else np.asarray(idx)
-        for e in idx_h.reshape(-1):
-            self.heat[(layer, int(e))] += 1
-        self.last[layer] = idx_h[-1].tolist()
-        y = self._moe(layer, x, idx, w)
-        self.moe_time += time.perf_counter() - t0
-        return y
+        start = time.perf_counter()
+        picks = _host(idx)
+        ids, counts = np.unique(picks, return_counts=True)
+        self.heat.update({(layer, int(e)): int(c) for e, c in zip(ids, counts)})
+        self.last[layer] = picks[-1].tolist()
+        result = self._moe(layer, x, idx, w)
+        self.moe_time += time.perf_counter() - start
+        return result
 
     def _moe(self, layer, x, idx, w):  # pragma: no cover - interface
         raise NotImplementedError
 
     def close(self) -> None:
-        pass
+        """Release what the backend holds (nothing for the local one)."""
 
 
 class LocalBackend(ExpertBackend):
-    """All experts resident in this GPU's HBM."""
+    """Every routed expert served by one ExpertStore (here: resident in this
+    GPU's HBM): the routing is regrouped per expert and handed to
+    ``store.compute``."""
 
     def __init__(self, store):
         super().__init__()
         self.store = store
 
     def _moe(self, layer, x, idx, w):
-        experts, offsets, rows, weights = group_by_expert(idx, w)
-        to_np = (lambda a: a.cpu().numpy()) if kernels.is_device(experts) else np.asarray
-        experts, offsets, rows, weights = map(to_np, (experts, offsets, rows, weights))
-        groups = [(experts[i], rows[offsets[i]:offsets[i + 1]], weights[offsets[i]:offsets[i + 1]])
-                  for i in range(len(experts))]
+        experts, offsets, rows, weights = (_host(a) for a in group_by_expert(idx, w))
+        cuts = offsets[1:-1]
+        groups = list(zip(experts, np.split(rows, cuts), np.split(weights, cuts)))
         return self.store.compute(layer, x, groups)
 
 
 def moe_layer(x, router, table, top_k: int, normalize: bool, H: int, I: int, gs: int, out=None, workspace=None):
-    """A whole MoE layer on the device for many rows (prompts): router product,
-    routing, grouping, the grouped MFMA expert FFN and the weighted combine.
-    ``table``: the layer's expert table (ExpertStore.layer_table)."""
+    """A prompt's whole MoE layer in one device call: router product, routing,
+    grouping, the grouped MFMA expert FFN and the weighted sum. ``table``: the
+    layer's device expert table (``ExpertStore.layer_table``)."""
     return kernels.prefill_layer(x, router, table, top_k, normalize, H, I, gs, out, workspace)

@@ -189,6 +189,61 @@ def test_q4_gemm_mfma(kernels, O, I, n):
     close_rows(kernels.q4_matmul_t_mfma(x, raw, s, 32, False), R.q4_matmul_t(x, raw, s, 32, False))
 
 
+# ---------------------------------------------------------------- range of the f16 operands
+
+def scaled_experts(rng, n, H, I, smag):
+    """int4 experts with f32 scales of magnitude ``smag``."""
+    out = []
+    for _ in range(n):
+        e = X.synthetic_expert(H, I, "int4", 32, rng, scale_dtype=np.float32)
+        e.gu.s = (rng.random(e.gu.s.shape) * smag).astype(np.float32)
+        e.down.s = (rng.random(e.down.s.shape) * smag).astype(np.float32)
+        out.append(e)
+    return out
+
+
+@pytest.mark.parametrize("xmag,smag", [(1e5, 2.5e-3), (1e3, 2.5e-3), (3e4, 2e-4), (1e-4, 2.5e-3)])
+def test_grouped_ffn_beyond_f16_range(kernels, xmag, smag):
+    """Rows far beyond f16's range (|x| ~ 1e5, with an outlier channel 40x
+    that), silu(gate) * up beyond it (|x| ~ 1e3 gives |gate|, |up| ~ 500), and
+    rows far below it (|x| ~ 1e-4): the gathered rows are scaled by a power of
+    two per row, silu(gate) * up per row and 64 columns, so every f16 operand
+    stays in range and the results within the tolerance of the f64 oracle."""
+    rng = np.random.default_rng(int(np.log10(xmag) * 10 + np.log10(smag)) % 1000)
+    H, I = 1024, 512
+    sizes = [3, 17, 40, 1]
+    ex = scaled_experts(rng, len(sizes), H, I, smag)
+    x = (rng.standard_normal((64, H)) * xmag).astype(np.float32)
+    x[5, 7] = 40 * xmag                      # an outlier channel
+    rows = [np.sort(rng.choice(64, n, replace=False)).astype(np.int32) for n in sizes]
+    eoff = np.zeros(len(sizes) + 1, np.int32)
+    np.cumsum(sizes, out=eoff[1:])
+    y = kernels.grouped_ffn(x, kernels.expert_table(ex), eoff, np.concatenate(rows), H, I, 32).cpu().numpy()
+    big = 0.0
+    for i, e in enumerate(ex):
+        Wgu, Wdn, inter = oracle_expert(e)
+        h = R.matmul_t_exact(x[rows[i]], Wgu)
+        big = max(big, np.abs(R.silu(h[:, :inter]) * h[:, inter:]).max())
+        close_rows(y[eoff[i]:eoff[i + 1]], R.expert_exact(x[rows[i]], Wgu, Wdn, inter))
+    if xmag >= 1e3 and smag > 1e-3:
+        assert big > 65504      # silu(gate) * up itself is beyond f16's range
+
+
+def test_q4_gemm_mfma_beyond_f16_range(kernels):
+    """The single-matrix MFMA product on f32 rows of ~1e5 with an outlier of
+    4e6, and on rows of ~1e-6: each 128-column piece of a row is scaled into
+    f16's range while it is staged."""
+    rng = np.random.default_rng(3)
+    O, I, n = 512, 1024, 24
+    raw = rng.integers(0, 256, (O, I // 2), dtype=np.uint8)
+    s = (np.abs(rng.normal(0, 0.02, (O, I // 32))) / 8).astype(np.float32)
+    x = rng.standard_normal((n, I)).astype(np.float32)
+    x[:12] *= 1e5
+    x[3, 100] = 4e6
+    x[12:] *= 1e-6
+    close_rows(kernels.q4_matmul_t_mfma(x, raw, s, 32, False), R.q4_matmul_t(x, raw, s, 32, False))
+
+
 # ---------------------------------------------------------------- whole layer
 
 def test_qwen3_30b_prefill_layer(kernels, c4_experts):
