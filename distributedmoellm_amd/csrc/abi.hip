@@ -529,8 +529,8 @@ MOE_API int moe_router_logits(const float* x, int ldx, const float* router, int 
 }
 
 MOE_API int moe_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, void* stream) {
-  REQUIRE(E > 0 && E <= 256, "moe_route: E=%d (1..256 experts)", E);
-  REQUIRE(k > 0 && k <= E && k <= 64, "moe_route: k=%d for E=%d", k, E);
+  REQUIRE(E > 0, "moe_route: E=%d", E);
+  REQUIRE(k > 0 && k <= E, "moe_route: k=%d for E=%d", k, E);
   REQUIRE(T >= 0, "moe_route: T=%d", T);
   if (T == 0) return MOE_OK;
   REQUIRE(logits && idx && w, "moe_route: null pointer");
@@ -539,7 +539,7 @@ MOE_API int moe_route(const float* logits, int T, int E, int k, int normalize, i
 
 MOE_API int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts,
                                 int* pos, int* experts, int* offsets, int* n_used, void* stream) {
-  REQUIRE(E > 0 && E <= 1024 && k > 0 && T >= 0, "moe_group_by_expert: T=%d k=%d E=%d", T, k, E);
+  REQUIRE(E > 0 && k > 0 && T >= 0, "moe_group_by_expert: T=%d k=%d E=%d", T, k, E);
   REQUIRE((long)T * k <= (1L << 30), "moe_group_by_expert: %d x %d picks", T, k);
   REQUIRE(idx && w && eoff && rows && wts && pos && experts && offsets && n_used, "moe_group_by_expert: null pointer");
   return run_group(idx, w, T, k, E, eoff, rows, wts, pos, experts, offsets, n_used, as_stream(stream));
@@ -592,7 +592,10 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
                               const moe_q4_expert* table, int H, int I, int gs, float* out, int ldo, void* workspace,
                               size_t ws_bytes, void* stream) {
   if (int rc = check_mfma_shape("moe_prefill_layer", H, I, gs)) return rc;
-  REQUIRE(E > 0 && E <= 256 && k > 0 && k <= E && k <= 16, "moe_prefill_layer: E=%d k=%d (E <= 256, k <= 16)", E, k);
+  REQUIRE(E > 0 && k > 0 && k <= E, "moe_prefill_layer: E=%d k=%d", E, k);
+  if (E > kMaxGridY || k > kCombineMaxPicks)
+    return set_error(MOE_EUNSUPPORTED, "moe_prefill_layer: E=%d k=%d (at most %d experts, %d picks a token)", E, k,
+                     kMaxGridY, kCombineMaxPicks);
   REQUIRE(T >= 0 && ldx >= H && ldo >= H, "moe_prefill_layer: T=%d ldx=%d ldo=%d", T, ldx, ldo);
   if (T == 0) return MOE_OK;
   REQUIRE(x && router && table && out, "moe_prefill_layer: null pointer");

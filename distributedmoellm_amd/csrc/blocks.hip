@@ -389,9 +389,11 @@ struct BQ6_K {
 // ---------------------------------------------------------------- the mat-vec kernel
 
 // L lanes per row (8..64), CPL chunks per lane; a wave covers 64/L rows a step
-// and ng steps. Waves are independent (no barrier).
+// and ng steps. Waves are independent (no barrier). The launch takes chunks
+// c0 .. c0+cn of every row (rows longer than L*CPL chunks take several
+// launches); acc: add to y instead of writing it.
 template <class F, int L, int CPL>
-__global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, int ng) {
+__global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, int ng, int c0, int cn, int acc) {
   constexpr int RPW = 64 / L;
   const int mat = blockIdx.y;
   int p0 = 0, p1 = job.n;
@@ -409,8 +411,8 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
   bool on[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    ch[c] = lc + c * L;
-    on[c] = ch[c] < sh.cpr;
+    ch[c] = c0 + lc + c * L;
+    on[c] = lc + c * L < cn;
   }
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
@@ -443,7 +445,10 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
         if (on[c]) a += F::dot(b[B][c], ch[c], xr[c]);
       a = lane_group_sum<L>(a);
       const int o = row_begin + it * RPW + lg;
-      if (lc == L - 1 && o < sh.O) job.y[(size_t)p * job.ldy + o] = a;
+      if (lc == L - 1 && o < sh.O) {
+        float* yo = job.y + (size_t)p * job.ldy + o;
+        *yo = acc ? *yo + a : a;
+      }
     };
     issue(B0{}, 0);
     int it = 0;
@@ -572,14 +577,16 @@ __global__ void dq_blocks_kernel(const uint8_t* raw, int O, int cols, float* out
 // ---------------------------------------------------------------- host side
 
 template <class F, int L, int CPL>
-void launch_blocks(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st) {
+void launch_blocks(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st, int c0 = 0, int cn = -1,
+                   int acc = 0) {
   constexpr int RPW = 64 / L;
   const long steps = (long)nmat * ((sh.O + RPW - 1) / RPW);
   int ng = (int)(steps / 2048);  // keep >= ~2048 waves in flight, amortise the activations
   ng = ng < 1 ? 1 : (ng > 16 ? 16 : ng);
   const int wave_rows = ng * RPW;
   const int waves = (sh.O + wave_rows - 1) / wave_rows;
-  hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL>), dim3((waves + 3) / 4, nmat), dim3(256), 0, st, sh, job, ng);
+  hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL>), dim3((waves + 3) / 4, nmat), dim3(256), 0, st, sh, job, ng, c0,
+                     cn < 0 ? sh.cpr : cn, acc);
 }
 
 // chunks a lane can hold activations for: 4 of the 32-value kinds, 2 of the 64-value
@@ -591,9 +598,15 @@ constexpr int max_cpl() {
 template <class F>
 int launch_fmt_blocks(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st) {
   const int cpr = sh.cpr;
-  if (cpr < 1 || cpr > 64 * max_cpl<F>())
-    return set_error(MOE_EUNSUPPORTED, "GGUF mat-vec: rows of %d values (at most %d of this type)", sh.I,
-                     64 * max_cpl<F>() * F::VALS);
+  if (cpr < 1) return set_error(MOE_EUNSUPPORTED, "GGUF mat-vec: rows of %d values", sh.I);
+  constexpr int seg = 64 * max_cpl<F>();  // chunks a lane group holds activations for
+  if (cpr > seg) {                        // long rows: one launch per segment, the later ones adding
+    for (int c0 = 0; c0 < cpr; c0 += seg) {
+      launch_blocks<F, 64, max_cpl<F>()>(sh, job, nmat, st, c0, cpr - c0 < seg ? cpr - c0 : seg, c0 > 0);
+      if (int rc = check_launch("GGUF block mat-vec (row segment)")) return rc;
+    }
+    return MOE_OK;
+  }
   if (cpr <= 8) launch_blocks<F, 8, 1>(sh, job, nmat, st);
   else if (cpr <= 16) launch_blocks<F, 16, 1>(sh, job, nmat, st);
   else if (cpr <= 32) launch_blocks<F, 32, 1>(sh, job, nmat, st);

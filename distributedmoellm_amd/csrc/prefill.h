@@ -37,6 +37,11 @@ struct GemmArgs {
   int ldaf_out;
 };
 
+// picks per token the token combine takes (its ordering lives in LDS)
+constexpr int kCombineMaxPicks = 4096;
+// experts per grouped-GEMM launch (one grid row each)
+constexpr int kMaxGridY = 65535;
+
 int router_slices(int T, int E, int H);
 int run_router_partials(const float* x, int ldx, const float* R, int T, int E, int H, int nz, float* part,
                         hipStream_t st);

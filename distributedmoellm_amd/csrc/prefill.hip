@@ -172,63 +172,170 @@ __device__ __forceinline__ void wave_best(float& v, int& i) {
   i = __builtin_amdgcn_readlane(i, 63);
 }
 
-// One wave per token: softmax over E <= 256 logits (f32: x - max, exp, / sum),
-// k picks by repeated arg-max (ties to the lower expert id, as a stable
-// descending sort), then w / sum(w) when normalising.
+// numpy's pairwise float32 sum of a[0..n) (the order of w.sum(-1) in the
+// reference's route): fewer than 8 values in sequence; up to 128 in 8 strided
+// partial sums, combined as ((0+1)+(2+3))+((4+5)+(6+7)), then the tail; longer
+// runs split at half (rounded down to a multiple of 8) and the halves added.
+// Explicit stack: eval entries push a value, combine entries add the last two.
+__device__ float pairwise_leaf(const float* a, int n) {
+  if (n < 8) {
+    float r = 0.f;
+    for (int i = 0; i < n; ++i) r += a[i];
+    return r;
+  }
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = a[j];
+  int i = 8;
+  for (; i < n - n % 8; i += 8)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res += a[i];
+  return res;
+}
+
+__device__ __noinline__ float pairwise_sum(const float* a, int n) {
+  int todo_off[64], todo_n[64];  // n < 0: combine
+  float val[32];
+  int nt = 0, nv = 0;
+  todo_off[nt] = 0;
+  todo_n[nt++] = n;
+  while (nt > 0) {
+    --nt;
+    const int o = todo_off[nt], m = todo_n[nt];
+    if (m < 0) {
+      const float r = val[--nv];
+      val[nv - 1] = val[nv - 1] + r;
+    } else if (m <= 128) {
+      val[nv++] = pairwise_leaf(a + o, m);
+    } else {
+      int h = m / 2;
+      h -= h % 8;
+      todo_n[nt++] = -1;  // runs after both halves
+      todo_off[nt] = o + h;
+      todo_n[nt++] = m - h;
+      todo_off[nt] = o;
+      todo_n[nt++] = h;  // left half first
+    }
+  }
+  return val[0];
+}
+
+// Order of the picks: larger probability first, then lower expert id (a
+// stable descending argsort); a NaN probability sorts after every number, as
+// numpy's argsort puts NaN last. key = p, or -1 for NaN (p >= 0 otherwise).
+__device__ __forceinline__ float pick_key(float p) { return p == p ? p : -1.f; }
+
+// One wave per token: softmax over the E logits (f32: x - max, exp, / sum),
+// then k picks, each the best (key, id) after the previous pick in that order
+// (no per-expert state, so E and k are not bounded), then w / sum(w) when
+// normalising, the sum in the reference's order. J > 0: the probabilities of
+// E <= 64 J experts stay in registers; J = 0: they are recomputed from the
+// logits in each pick round (the same operations, so the same values).
+// Picks r < 64 are kept by lane r and written together; with k > 64 lane 0
+// writes every pick as it is found and normalises them afterwards, reading
+// back its own writes.
+template <int J>
 __global__ __launch_bounds__(256) void route_kernel(const float* logits, int nz, int T, int E, int k, int normalize,
                                                     int* idx, float* w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float* lg = logits + (size_t)t * E;
-  float v[4];
+  auto logit = [&](int e) {
+    float l = lg[e];
+    for (int z = 1; z < nz; ++z) l += lg[(size_t)z * T * E + e];  // K slices, in order
+    return l;
+  };
+  constexpr int JR = J > 0 ? J : 1;
+  float v[JR];
   float m = -INFINITY;
+  if constexpr (J > 0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    float l = -INFINITY;
-    if (e < E) {
-      l = lg[e];
-      for (int z = 1; z < nz; ++z) l += lg[(size_t)z * T * E + e];  // K slices, in order
+    for (int j = 0; j < J; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = e < E ? logit(e) : -INFINITY;
+      m = fmaxf(m, v[j]);
     }
-    v[j] = l;
-    m = fmaxf(m, v[j]);
+  } else {
+    for (int e = lane; e < E; e += 64) m = fmaxf(m, logit(e));
   }
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   float s = 0.f;
+  if constexpr (J > 0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = e < E ? expf(v[j] - m) : 0.f;
-    s += v[j];
+    for (int j = 0; j < J; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = e < E ? expf(v[j] - m) : 0.f;
+      s += v[j];
+    }
+  } else {
+    for (int e = lane; e < E; e += 64) s += expf(logit(e) - m);
   }
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if constexpr (J > 0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = v[j] / s;  // probabilities, f32
-  bool taken[4] = {false, false, false, false};
-  float wsum = 0.f, picked = 0.f;
-  int mine = -1;  // lane r keeps pick r
+    for (int j = 0; j < J; ++j) v[j] = v[j] / s;  // probabilities, f32
+  }
+  // numpy's pairwise order for k <= 128, accumulated as the picks come:
+  // acc[0] takes pick r < k - k % 8 and the eight rotate (8 steps restore them)
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+  const int nb = k < 8 ? 0 : k - k % 8;
+  float pk = INFINITY;  // the previous pick: key, id
+  int pi = -1;
+  float picked = 0.f;
+  int mine = -1;
   for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
+    float bk = -INFINITY;
     int bi = 0x7fffffff;
+    auto consider = [&](float p, int e) {
+      const float key = pick_key(p);
+      if (key < pk || (key == pk && e > pi)) better(bk, bi, key, e);
+    };
+    if constexpr (J > 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && !taken[j]) better(bv, bi, v[j], e);
+      for (int j = 0; j < J; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) consider(v[j], e);
+      }
+    } else {
+      for (int e = lane; e < E; e += 64) consider(expf(logit(e) - m) / s, e);
     }
-    wave_best(bv, bi);
+    wave_best(bk, bi);
+    pk = bk;
+    pi = bi;
+    const float p = bk < 0.f ? __builtin_nanf("") : bk;
+    if (r < nb) {
+      acc[0] += p;
+      const float a0 = acc[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (lane + 64 * j == bi) taken[j] = true;
-    wsum += bv;
-    if (lane == r) {
-      mine = bi;
-      picked = bv;
+      for (int j = 0; j < 7; ++j) acc[j] = acc[j + 1];
+      acc[7] = a0;
+      if (r == nb - 1) wsum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    } else {
+      wsum += p;
+    }
+    if (k <= 64) {
+      if (lane == r) {
+        mine = bi;
+        picked = p;
+      }
+    } else if (lane == 0) {
+      idx[(size_t)t * k + r] = bi;
+      w[(size_t)t * k + r] = p;
     }
   }
-  if (lane < k) {
-    idx[(size_t)t * k + lane] = mine;
-    w[(size_t)t * k + lane] = normalize ? picked / wsum : picked;
+  if (k <= 64) {
+    if (lane < k) {
+      idx[(size_t)t * k + lane] = mine;
+      w[(size_t)t * k + lane] = normalize ? picked / wsum : picked;
+    }
+  } else if (normalize && lane == 0) {
+    float* wt = w + (size_t)t * k;
+    if (k > 128) wsum = pairwise_sum(wt, k);
+    for (int r = 0; r < k; ++r) wt[r] = wt[r] / wsum;
   }
 }
 
@@ -331,27 +438,35 @@ __global__ __launch_bounds__(256) void group_kernel(const int* idx, const float*
   }
 }
 
-// The experts that received picks, ascending, with their ranges (E <= 1024).
+// The experts that received picks, ascending, with their ranges: one block
+// walks the experts 1024 at a time, carrying the count so far.
 __global__ __launch_bounds__(1024) void used_experts_kernel(const int* eoff, int E, int* experts, int* offsets,
                                                             int* n_used) {
   __shared__ int wave_used[16];
-  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
-  const bool used = e < E && eoff[e + 1] > eoff[e];
-  const uint64_t m = __ballot(used);
-  if (lane == 0) wave_used[wave] = __popcll(m);
-  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int base = 0;
-  for (int i = 0; i < wave; ++i) base += wave_used[i];
-  if (used) {
-    const int slot = base + __popcll(m & ((1ull << lane) - 1ull));
-    experts[slot] = e;
-    offsets[slot] = eoff[e];
+  for (int e0 = 0; e0 < E; e0 += 1024) {
+    const int e = e0 + threadIdx.x;
+    const bool used = e < E && eoff[e + 1] > eoff[e];
+    const uint64_t m = __ballot(used);
+    if (lane == 0) wave_used[wave] = __popcll(m);
+    __syncthreads();
+    int before = base, all = base;
+    for (int i = 0; i < 16; ++i) {
+      before += i < wave ? wave_used[i] : 0;
+      all += wave_used[i];
+    }
+    if (used) {
+      const int slot = before + __popcll(m & ((1ull << lane) - 1ull));
+      experts[slot] = e;
+      offsets[slot] = eoff[e];
+    }
+    base = all;
+    __syncthreads();  // wave_used is rewritten by the next round
   }
-  if (e == 0) {
-    int total = 0;
-    for (int i = 0; i < 16; ++i) total += wave_used[i];
-    *n_used = total;
-    offsets[total] = eoff[E];
+  if (threadIdx.x == 0) {
+    *n_used = base;
+    offsets[base] = eoff[E];
   }
 }
 
@@ -894,31 +1009,58 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
 
 // out[t] = sum over t's picks in ascending expert order (= ascending pair
 // position) of w * y[pos]; overwrites out (the layer output starts at zero).
-// One block per token: the first wave ranks the token's (at most 16) picks by
-// position -- rank = number of smaller positions, positions being distinct --
-// and puts them in LDS in that order; then each thread sums float4 columns
-// over the picks in order.
+// One block per token. The picks are put in LDS in position order -- a pick's
+// rank is the number of smaller positions, positions being distinct: for
+// k <= 64 the first wave ranks them with shuffles; for more, the block stages
+// the positions in dynamic LDS (12 bytes a pick) and every thread ranks its
+// picks against them. Then each thread sums float4 columns over the picks in
+// order.
 __global__ __launch_bounds__(256) void token_combine_kernel(const float* y, int ldy, const int* pos, const float* wts,
                                                             int k, int H, float* out, int ldo, int vec4) {
-  __shared__ int sp[16];
-  __shared__ float sw[16];
+  __shared__ int sp64[64];
+  __shared__ float sw64[64];
   __shared__ int sn;
+  extern __shared__ int dyn[];  // k > 64: raw positions [k], ordered positions [k], weights [k]
   const int t = blockIdx.x;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const bool mine = lane < k && lane < 16;
-    const int p = mine ? pos[(size_t)t * k + lane] : -1;
-    int rank = 0;
-    for (int i = 0; i < k && i < 16; ++i) {
-      const int pi = __shfl(p, i, 64);
-      rank += (pi >= 0 && pi < p) ? 1 : 0;
+  const int* prow = pos + (size_t)t * k;
+  int* sp = sp64;
+  float* sw = sw64;
+  if (k <= 64) {
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      const bool mine = lane < k;
+      const int p = mine ? prow[lane] : -1;
+      int rank = 0;
+      for (int i = 0; i < k; ++i) {
+        const int pi = __shfl(p, i, 64);
+        rank += (pi >= 0 && pi < p) ? 1 : 0;
+      }
+      const uint64_t valid = __ballot(mine && p >= 0);
+      if (mine && p >= 0) {
+        sp[rank] = p;
+        sw[rank] = wts[p];
+      }
+      if (lane == 0) sn = __popcll(valid);
     }
-    const uint64_t valid = __ballot(mine && p >= 0);
-    if (mine && p >= 0) {
+  } else {
+    int* raw = dyn;
+    sp = dyn + k;
+    sw = reinterpret_cast<float*>(dyn + 2 * k);
+    if (threadIdx.x == 0) sn = 0;
+    for (int i = threadIdx.x; i < k; i += 256) raw[i] = prow[i];
+    __syncthreads();
+    int valid = 0;
+    for (int i = threadIdx.x; i < k; i += 256) {
+      const int p = raw[i];
+      if (p < 0) continue;
+      int rank = 0;
+      for (int j = 0; j < k; ++j) rank += (raw[j] >= 0 && raw[j] < p) ? 1 : 0;
       sp[rank] = p;
       sw[rank] = wts[p];
+      ++valid;
     }
-    if (lane == 0) sn = __popcll(valid);
+    for (int off = 32; off > 0; off >>= 1) valid += __shfl_xor(valid, off, 64);
+    if ((threadIdx.x & 63) == 0) atomicAdd(&sn, valid);
   }
   __syncthreads();
   const int n = sn;
@@ -1015,7 +1157,11 @@ int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int
 }
 
 int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st) {
-  hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, nz, T, E, k, normalize, idx, w);
+  if (T <= 0) return MOE_OK;
+  const dim3 grid((T + 3) / 4), block(256);
+  if (E <= 256) hipLaunchKernelGGL(route_kernel<4>, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w);
+  else if (E <= 1024) hipLaunchKernelGGL(route_kernel<16>, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w);
+  else hipLaunchKernelGGL(route_kernel<0>, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w);
   return check_launch("softmax top-k");
 }
 
@@ -1036,6 +1182,8 @@ int run_gather_f16(const float* x, int ldx, const int* rows, int P, int K, _Floa
 
 int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
   if (nexp <= 0) return MOE_OK;
+  if (nexp > kMaxGridY)
+    return set_error(MOE_EUNSUPPORTED, "int4 grouped GEMM: %d experts (at most %d a launch)", nexp, kMaxGridY);
   const int per_tile = mode == MODE_GATE_UP ? 64 : 128;
   const int n = mode == MODE_GATE_UP ? a.I : a.N;
   dim3 grid((n + per_tile - 1) / per_tile, nexp);
@@ -1054,9 +1202,11 @@ int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
 int run_token_combine(const float* y, int ldy, const int* pos, const float* wts, int T, int k, int H, float* out,
                       int ldo, hipStream_t st) {
   if (T <= 0) return MOE_OK;
-  if (k > 16) return set_error(MOE_EINVAL, "token combine: k=%d (at most 16 picks per token)", k);
+  if (k > kCombineMaxPicks)
+    return set_error(MOE_EUNSUPPORTED, "token combine: k=%d (at most %d picks per token)", k, kCombineMaxPicks);
   const int vec4 = H % 4 == 0 && ldy % 4 == 0 && ldo % 4 == 0 && aligned(y, 16) && aligned(out, 16);
-  hipLaunchKernelGGL(token_combine_kernel, dim3(T), dim3(256), 0, st, y, ldy, pos, wts, k, H, out, ldo, vec4);
+  const size_t lds = k > 64 ? (size_t)12 * k : 0;
+  hipLaunchKernelGGL(token_combine_kernel, dim3(T), dim3(256), lds, st, y, ldy, pos, wts, k, H, out, ldo, vec4);
   return check_launch("token combine");
 }
 

@@ -80,7 +80,8 @@ int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* s, int s
                     float* y, void* stream);
 
 /* y[n, O] = x[n, cols] @ W.T for GGUF block-quantized rows of any quantized
- * type, cols <= 8192; rows need no alignment.
+ * type, any cols (rows past 8192 values take one launch per 8192-value
+ * segment, summed in segment order); rows need no alignment.
  * Replaces gguf_matmul_t(x, raw, qtype, cols), moelan/kernels.py:981-998
  * (_mv_q8_0 :482-498, _mv_q4_k :499-528, _mv_q5_k :529-561, _mv_q6_k
  * :562-596, _mv_q2_k :597-632, _mv_q3_k :642-677, _gguf_mm :678-691). */
@@ -230,16 +231,17 @@ int moe_router_logits(const float* x, int ldx, const float* router, int T, int E
                       void* workspace, size_t ws_bytes, void* stream);
 
 /* Softmax router with top-k: idx[T, k] int32, w[T, k] f32, largest first,
- * ties to the lower expert id; w renormalised to sum 1 when normalize != 0.
- * E <= 256, k <= 64. Replaces route(), moelan/model.py:154-167 (softmax :83-86). */
+ * ties to the lower expert id, NaN probabilities last; w divided by its sum
+ * (numpy's pairwise summation order) when normalize != 0. Any E, 1 <= k <= E.
+ * Replaces route(), moelan/model.py:154-167 (softmax :83-86). */
 int moe_route(const float* logits, int T, int E, int k, int normalize, int* idx, float* w, void* stream);
 
 /* Stable grouping of the T*k picks by expert, as group_by_expert(),
  * moelan/model.py:226-236: experts[0..*n_used) ascending with their pick
  * ranges offsets[0..*n_used]; eoff[E+1] the same ranges for every expert id;
  * rows[q] / wts[q] the token and weight of grouped pick q; pos[t*k+j] where
- * pick j of token t went (-1 for an expert id outside 0..E-1). E <= 1024.
- * All device arrays. */
+ * pick j of token t went (-1 for an expert id outside 0..E-1). All device
+ * arrays. */
 int moe_group_by_expert(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
                         int* experts, int* offsets, int* n_used, void* stream);
 
@@ -251,7 +253,8 @@ size_t moe_q4_grouped_ffn_workspace(int P, int H, int I);
  * Expert.__call__, moelan/experts.py:256-259, on many rows at once, as the
  * reference's big-group path (dequant + BLAS, moelan/experts.py:216-219,
  * 718-723). int4 -> f16 in registers, f16 MFMA with f32 accumulation
- * (relative error ~1e-3 at most). H, I multiples of 128; gs a multiple of 32. */
+ * (relative error ~1e-3 at most). H, I multiples of 128; gs a multiple of 32;
+ * nexp <= 65535. */
 int moe_q4_grouped_ffn(const float* x, int ldx, const moe_q4_expert* table, int nexp, const int* eoff, const int* rows,
                        int P, int H, int I, int gs, float* y, int ldy, void* workspace, size_t ws_bytes, void* stream);
 
@@ -262,7 +265,8 @@ size_t moe_prefill_workspace(int T, int E, int k, int H, int I);
  * FFN, weighted combine; out[t] = sum over t's k experts (ascending id) of
  * w * expert(x[t]) (written, not added). table[e] is expert e of the layer.
  * MoEModel._ffn + LocalBackend._moe + ExpertStore.compute for a prompt,
- * moelan/model.py:597-606, 274-278, moelan/experts.py:641-670. */
+ * moelan/model.py:597-606, 274-278, moelan/experts.py:641-670.
+ * E <= 65535 experts, k <= 4096 picks a token. */
 int moe_prefill_layer(const float* x, int ldx, const float* router, int T, int E, int k, int normalize,
                       const moe_q4_expert* table, int H, int I, int gs, float* out, int ldo, void* workspace,
                       size_t ws_bytes, void* stream);

@@ -79,9 +79,15 @@ def test_unsupported_is_its_own_code():
     assert L.moe_gguf_matmul_t(1, 1, 1, 30, 8, 256, 1, None) == _lib.MOE_EUNSUPPORTED    # BF16
     assert L.moe_gguf_dequant(1, 9, 8, 32, 1, None) == _lib.MOE_EUNSUPPORTED            # Q8_1
     assert L.moe_gguf_dequant(1, 1, 8, 32, 1, None) == _lib.MOE_EUNSUPPORTED            # F16
-    # rows of more than 8192 values are not taken by the block mat-vec (nothing launched)
-    assert L.moe_gguf_matmul_t(1, 1, 1, 14, 8, 256 * 33, 1, None) == _lib.MOE_EUNSUPPORTED
-    assert L.moe_gguf_matmul_t(1, 1, 1, 2, 8, 32 * 257, 1, None) == _lib.MOE_EUNSUPPORTED
+    # a prompt layer over more experts than a launch has grid rows, or with more
+    # picks a token than the combine orders in LDS (nothing launched)
+    args = (1, 128, 1, 4)
+    assert L.moe_prefill_layer(*args, 70000, 8, 1, 1, 128, 128, 32, 1, 128, 1, 1 << 20, None) == \
+        _lib.MOE_EUNSUPPORTED
+    assert L.moe_prefill_layer(*args, 8192, 5000, 1, 1, 128, 128, 32, 1, 128, 1, 1 << 20, None) == \
+        _lib.MOE_EUNSUPPORTED
+    assert L.moe_prefill_layer(*args, 64, 65, 1, 1, 128, 128, 32, 1, 128, 1, 1 << 20, None) == _lib.MOE_EINVAL
+    assert L.moe_route(1, 4, 64, 65, 1, 1, 1, None) == _lib.MOE_EINVAL     # k > E
     # every quantized type is taken; its rows must hold whole blocks
     for qt, per in ((2, 32), (3, 32), (6, 32), (7, 32), (10, 256), (11, 256), (13, 256), (14, 256)):
         assert L.moe_gguf_matmul_t(1, 1, 1, qt, 8, per + 16, 1, None) == _lib.MOE_EINVAL

@@ -207,7 +207,7 @@ def test_grouped_ffn_beyond_f16_range(kernels, xmag, smag):
     """Rows far beyond f16's range (|x| ~ 1e5, with an outlier channel 40x
     that), silu(gate) * up beyond it (|x| ~ 1e3 gives |gate|, |up| ~ 500), and
     rows far below it (|x| ~ 1e-4): the gathered rows are scaled by a power of
-    two per row, silu(gate) * up per row and 64 columns, so every f16 operand
+    two per row, silu(gate) * up per row and 16 columns, so every f16 operand
     stays in range and the results within the tolerance of the f64 oracle."""
     rng = np.random.default_rng(int(np.log10(xmag) * 10 + np.log10(smag)) % 1000)
     H, I = 1024, 512
