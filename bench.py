@@ -672,20 +672,20 @@ def stack_decode(args, L, batches=(1, 8, 32)):
         ms = float(np.median([a.elapsed_time(b) for a, b in evs]))
         # the same steps captured as HIP graphs (one per routing variant) and replayed
         graphs = []
-        for v in range(nvar):
+        for v in range(nvar if not args.no_graph else 0):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 step(v, torch.cuda.current_stream().cuda_stream)
             graphs.append(g)
         torch.cuda.synchronize()
         gevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
-        for s_ in range(nsteps):
+        for s_ in range(nsteps if graphs else 0):
             x.normal_()
             gevs[s_][0].record()
             graphs[s_ % nvar].replay()
             gevs[s_][1].record()
         torch.cuda.synchronize()
-        ms_graph = float(np.median([a.elapsed_time(b) for a, b in gevs]))
+        ms_graph = float(np.median([a.elapsed_time(b) for a, b in gevs])) if graphs else float("nan")
         del graphs
         avg_bytes = float(step_bytes.mean())
         key = f"B{B}"
@@ -803,6 +803,8 @@ def main() -> int:
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--batches", default="1,8,32", help="token batches of the 235B-shaped stack decode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay figure of the stack decode "
+                                                            "(for counter runs)")
     ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, wire, residency, prefill, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()

@@ -391,8 +391,10 @@ struct BQ6_K {
 // L lanes per row (8..64), CPL chunks per lane; a wave covers 64/L rows a step
 // and ng steps. Waves are independent (no barrier). The launch takes chunks
 // c0 .. c0+cn of every row (rows longer than L*CPL chunks take several
-// launches); acc: add to y instead of writing it.
-template <class F, int L, int CPL>
+// launches); acc: add to y instead of writing it. NR input rows share each
+// pass over the weights (their activations held together), so a matrix's
+// blocks are read once per NR rows.
+template <class F, int L, int CPL, int NR>
 __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, int ng, int c0, int cn, int acc) {
   constexpr int RPW = 64 / L;
   const int mat = blockIdx.y;
@@ -416,16 +418,21 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
   }
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  for (int p = p0; p < p1; ++p) {
-    const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
-    float xr[CPL][F::XR];
+  // grid.z splits the input rows: slice z takes batches z, z + gridDim.z, ...
+  for (int pb = p0 + (int)blockIdx.z * NR; pb < p1; pb += NR * (int)gridDim.z) {
+    float xr[NR][CPL][F::XR];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      if (on[c]) {
-        F::load_x(xs, ch[c], xr[c]);
-      } else {
+    for (int r = 0; r < NR; ++r) {
+      const int p = pb + r < p1 ? pb + r : p1 - 1;  // rows past the end repeat the last (not stored)
+      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
 #pragma unroll
-        for (int j = 0; j < F::XR; ++j) xr[c][j] = 0.f;
+      for (int c = 0; c < CPL; ++c) {
+        if (on[c]) {
+          F::load_x(xs, ch[c], xr[r][c]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+        }
       }
     }
     typename F::Blk b[2][CPL];
@@ -439,15 +446,18 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
     };
     auto compute = [&](auto buf, int it) {
       constexpr int B = decltype(buf)::value;
-      float a = 0.f;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c)
-        if (on[c]) a += F::dot(b[B][c], ch[c], xr[c]);
-      a = lane_group_sum<L>(a);
       const int o = row_begin + it * RPW + lg;
-      if (lc == L - 1 && o < sh.O) {
-        float* yo = job.y + (size_t)p * job.ldy + o;
-        *yo = acc ? *yo + a : a;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float a = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+          if (on[c]) a += F::dot(b[B][c], ch[c], xr[r][c]);
+        a = lane_group_sum<L>(a);
+        if (lc == L - 1 && o < sh.O && pb + r < p1) {
+          float* yo = job.y + (size_t)(pb + r) * job.ldy + o;
+          *yo = acc ? *yo + a : a;
+        }
       }
     };
     issue(B0{}, 0);
@@ -576,17 +586,18 @@ __global__ void dq_blocks_kernel(const uint8_t* raw, int O, int cols, float* out
 
 // ---------------------------------------------------------------- host side
 
-template <class F, int L, int CPL>
+template <class F, int L, int CPL, int NR = 1>
 void launch_blocks(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st, int c0 = 0, int cn = -1,
-                   int acc = 0) {
+                   int acc = 0, int max_rows = 1) {
   constexpr int RPW = 64 / L;
   const long steps = (long)nmat * ((sh.O + RPW - 1) / RPW);
   int ng = (int)(steps / 2048);  // keep >= ~2048 waves in flight, amortise the activations
   ng = ng < 1 ? 1 : (ng > 16 ? 16 : ng);
   const int wave_rows = ng * RPW;
   const int waves = (sh.O + wave_rows - 1) / wave_rows;
-  hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL>), dim3((waves + 3) / 4, nmat), dim3(256), 0, st, sh, job, ng, c0,
-                     cn < 0 ? sh.cpr : cn, acc);
+  hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL, NR>),
+                     dim3((waves + 3) / 4, nmat, row_slices(max_rows, NR, (long)waves * nmat)), dim3(256), 0, st, sh,
+                     job, ng, c0, cn < 0 ? sh.cpr : cn, acc);
 }
 
 // chunks a lane can hold activations for: 4 of the 32-value kinds, 2 of the 64-value
@@ -595,24 +606,41 @@ constexpr int max_cpl() {
   return F::XR > 40 ? 2 : 4;
 }
 
+// input rows a pass holds: 4 with one chunk of a 32-value kind per lane, 2
+// with one 64-value chunk or two 32-value ones, else 1
+template <class F, int CPL>
+constexpr int rows_per_pass() {
+  return F::XR * CPL <= 40 ? 4 : (F::XR * CPL <= 80 ? 2 : 1);
+}
+
+template <class F, int L, int CPL>
+void launch_rows(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st, int c0 = 0, int cn = -1,
+                 int acc = 0) {
+  constexpr int NR = rows_per_pass<F, CPL>();
+  if (NR >= 4 && max_rows >= 3) launch_blocks<F, L, CPL, NR>(sh, job, nmat, st, c0, cn, acc, max_rows);
+  else if (NR >= 2 && max_rows >= 2)
+    launch_blocks<F, L, CPL, (NR >= 2 ? 2 : 1)>(sh, job, nmat, st, c0, cn, acc, max_rows);
+  else launch_blocks<F, L, CPL, 1>(sh, job, nmat, st, c0, cn, acc, max_rows);
+}
+
 template <class F>
-int launch_fmt_blocks(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st) {
+int launch_fmt_blocks(const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   const int cpr = sh.cpr;
   if (cpr < 1) return set_error(MOE_EUNSUPPORTED, "GGUF mat-vec: rows of %d values", sh.I);
   constexpr int seg = 64 * max_cpl<F>();  // chunks a lane group holds activations for
   if (cpr > seg) {                        // long rows: one launch per segment, the later ones adding
     for (int c0 = 0; c0 < cpr; c0 += seg) {
-      launch_blocks<F, 64, max_cpl<F>()>(sh, job, nmat, st, c0, cpr - c0 < seg ? cpr - c0 : seg, c0 > 0);
+      launch_rows<F, 64, max_cpl<F>()>(sh, job, nmat, max_rows, st, c0, cpr - c0 < seg ? cpr - c0 : seg, c0 > 0);
       if (int rc = check_launch("GGUF block mat-vec (row segment)")) return rc;
     }
     return MOE_OK;
   }
-  if (cpr <= 8) launch_blocks<F, 8, 1>(sh, job, nmat, st);
-  else if (cpr <= 16) launch_blocks<F, 16, 1>(sh, job, nmat, st);
-  else if (cpr <= 32) launch_blocks<F, 32, 1>(sh, job, nmat, st);
-  else if (cpr <= 64) launch_blocks<F, 64, 1>(sh, job, nmat, st);
-  else if (cpr <= 128) launch_blocks<F, 64, 2>(sh, job, nmat, st);
-  else if constexpr (max_cpl<F>() >= 4) launch_blocks<F, 64, 4>(sh, job, nmat, st);
+  if (cpr <= 8) launch_rows<F, 8, 1>(sh, job, nmat, max_rows, st);
+  else if (cpr <= 16) launch_rows<F, 16, 1>(sh, job, nmat, max_rows, st);
+  else if (cpr <= 32) launch_rows<F, 32, 1>(sh, job, nmat, max_rows, st);
+  else if (cpr <= 64) launch_rows<F, 64, 1>(sh, job, nmat, max_rows, st);
+  else if (cpr <= 128) launch_rows<F, 64, 2>(sh, job, nmat, max_rows, st);
+  else if constexpr (max_cpl<F>() >= 4) launch_rows<F, 64, 4>(sh, job, nmat, max_rows, st);
   return check_launch("GGUF block mat-vec");
 }
 
@@ -650,19 +678,19 @@ bool block_geometry(int qtype, int* per, int* size, int* vals) {
   return false;
 }
 
-int run_matvec_blocks(int qtype, const MVShape& sh, const MVJob& job, int nmat, hipStream_t st) {
+int run_matvec_blocks(int qtype, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   if (nmat <= 0 || sh.O <= 0) return MOE_OK;
   switch (qtype) {
-    case FMT_Q8_0: return launch_fmt_blocks<BQ8_0>(sh, job, nmat, st);
-    case FMT_Q4_K: return launch_fmt_blocks<BQ4_K>(sh, job, nmat, st);
-    case FMT_Q4_0: return launch_fmt_blocks<BQ4_0>(sh, job, nmat, st);
-    case FMT_Q4_1: return launch_fmt_blocks<BQ4_1>(sh, job, nmat, st);
-    case FMT_Q5_0: return launch_fmt_blocks<BQ5_0>(sh, job, nmat, st);
-    case FMT_Q5_1: return launch_fmt_blocks<BQ5_1>(sh, job, nmat, st);
-    case FMT_Q2_K: return launch_fmt_blocks<BQ2_K>(sh, job, nmat, st);
-    case FMT_Q3_K: return launch_fmt_blocks<BQ3_K>(sh, job, nmat, st);
-    case FMT_Q5_K: return launch_fmt_blocks<BQ5_K>(sh, job, nmat, st);
-    case FMT_Q6_K: return launch_fmt_blocks<BQ6_K>(sh, job, nmat, st);
+    case FMT_Q8_0: return launch_fmt_blocks<BQ8_0>(sh, job, nmat, max_rows, st);
+    case FMT_Q4_K: return launch_fmt_blocks<BQ4_K>(sh, job, nmat, max_rows, st);
+    case FMT_Q4_0: return launch_fmt_blocks<BQ4_0>(sh, job, nmat, max_rows, st);
+    case FMT_Q4_1: return launch_fmt_blocks<BQ4_1>(sh, job, nmat, max_rows, st);
+    case FMT_Q5_0: return launch_fmt_blocks<BQ5_0>(sh, job, nmat, max_rows, st);
+    case FMT_Q5_1: return launch_fmt_blocks<BQ5_1>(sh, job, nmat, max_rows, st);
+    case FMT_Q2_K: return launch_fmt_blocks<BQ2_K>(sh, job, nmat, max_rows, st);
+    case FMT_Q3_K: return launch_fmt_blocks<BQ3_K>(sh, job, nmat, max_rows, st);
+    case FMT_Q5_K: return launch_fmt_blocks<BQ5_K>(sh, job, nmat, max_rows, st);
+    case FMT_Q6_K: return launch_fmt_blocks<BQ6_K>(sh, job, nmat, max_rows, st);
   }
   return set_error(MOE_EUNSUPPORTED, "GGUF mat-vec: qtype %d", qtype);
 }

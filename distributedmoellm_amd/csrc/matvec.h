@@ -75,6 +75,9 @@ __device__ __forceinline__ MatRef resolve(const MVJob& job, int mat) {
 }
 
 int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh);
+// grid.z slices of the input rows for a launch of `waves` waves taking NR rows
+// a pass: 1 .. ceil(max_rows / NR), about 16K waves in all
+int row_slices(int max_rows, int NR, long waves);
 // rows xrow[p] (or p) of x, or silu(h[:, :half]) * h[:, half:] when half > 0,
 // rounded to int8 per group of gs (a multiple of 64 up to 512): q [n, K] bytes,
 // each 32-column chunk as its 16 even columns then its 16 odd ones; d, s8 [n, K/gs]

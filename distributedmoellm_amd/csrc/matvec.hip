@@ -198,7 +198,8 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
   const uint8_t* const W = M.w;
   const void* const S = M.s;
 
-  for (int pb = p0; pb < p1; pb += NR) {
+  // grid.z splits the input rows: slice z takes batches z, z + gridDim.z, ...
+  for (int pb = p0 + (int)blockIdx.z * NR; pb < p1; pb += NR * (int)gridDim.z) {
     float xr[NR][CPL][F::XR];
     uint4 wb[2][G][CPL];
     uint32_t sb[2][G][CPL];
@@ -997,9 +998,20 @@ static void launch_fmt(const MVShape& sh, const MVJob& job, int nmat, int max_ro
   else launch_nr<F, 4, P>(sh, job, nmat, st);
 }
 
+// Slices of the input rows (grid.z) for a launch of `waves` waves: with few
+// waves and many row batches of NR, each wave would stream its weights once
+// per batch in sequence; slices run the batches side by side (the weights are
+// read again from L2 or the MALL), up to ~16K waves in all.
+int row_slices(int max_rows, int NR, long waves) {
+  const long batches = (max_rows + NR - 1) / NR;
+  long z = 16384 / (waves > 0 ? waves : 1);
+  z = z < 1 ? 1 : (z > batches ? batches : z);
+  return (int)(z > 65535 ? 65535 : z);
+}
+
 template <class F, int L, int CPL>
-static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr, int A, hipStream_t st) {
-  auto go = [&](auto kernel, int G) {
+static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr, int max_rows, int A, hipStream_t st) {
+  auto go = [&](auto kernel, int G, int NR) {
     constexpr int rpp = 64 / L;
     const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));  // wave groups in the launch
     // runs of several groups per wave amortise the activation set-up; keep
@@ -1015,12 +1027,12 @@ static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr,
     ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
     const int wave_rows = ng * G * rpp;
     const int waves = (sh.O + wave_rows - 1) / wave_rows;
-    dim3 grid((waves + 3) / 4, nmat);
+    dim3 grid((waves + 3) / 4, nmat, row_slices(max_rows, NR, (long)waves * nmat));
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, sh, job, A, ng);
   };
-  if (nr == 1) go(mv_fast_kernel<F, L, CPL, 1>, fast_group<CPL, 1>());
-  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, L, CPL, 2>, fast_group<CPL, 2>());
-  else go(mv_fast_kernel<F, L, 1, 4>, fast_group<1, 4>());
+  if (nr == 1) go(mv_fast_kernel<F, L, CPL, 1>, fast_group<CPL, 1>(), 1);
+  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, L, CPL, 2>, fast_group<CPL, 2>(), 2);
+  else go(mv_fast_kernel<F, L, 1, 4>, fast_group<1, 4>(), 4);
 }
 
 // Lanes per row: by default one chunk per lane whenever a row has at most 64
@@ -1063,17 +1075,17 @@ static bool launch_fast(const MVShape& sh, const MVJob& job, int nmat, int max_r
   const int nr = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
   if (L == 64) {
     switch (cpl) {
-      case 1: launch_fast_l<F, 64, 1>(sh, job, nmat, nr, A, st); return true;
-      case 2: launch_fast_l<F, 64, 2>(sh, job, nmat, nr, A, st); return true;
-      case 3: launch_fast_l<F, 64, 3>(sh, job, nmat, nr, A, st); return true;
-      case 4: launch_fast_l<F, 64, 4>(sh, job, nmat, nr, A, st); return true;
+      case 1: launch_fast_l<F, 64, 1>(sh, job, nmat, nr, max_rows, A, st); return true;
+      case 2: launch_fast_l<F, 64, 2>(sh, job, nmat, nr, max_rows, A, st); return true;
+      case 3: launch_fast_l<F, 64, 3>(sh, job, nmat, nr, max_rows, A, st); return true;
+      case 4: launch_fast_l<F, 64, 4>(sh, job, nmat, nr, max_rows, A, st); return true;
     }
     return false;
   }
-  if (L == 32 && cpl == 1) { launch_fast_l<F, 32, 1>(sh, job, nmat, nr, A, st); return true; }
-  if (L == 32 && cpl == 2) { launch_fast_l<F, 32, 2>(sh, job, nmat, nr, A, st); return true; }
-  if (L == 16 && cpl == 1) { launch_fast_l<F, 16, 1>(sh, job, nmat, nr, A, st); return true; }
-  if (L == 8 && cpl == 1) { launch_fast_l<F, 8, 1>(sh, job, nmat, nr, A, st); return true; }
+  if (L == 32 && cpl == 1) { launch_fast_l<F, 32, 1>(sh, job, nmat, nr, max_rows, A, st); return true; }
+  if (L == 32 && cpl == 2) { launch_fast_l<F, 32, 2>(sh, job, nmat, nr, max_rows, A, st); return true; }
+  if (L == 16 && cpl == 1) { launch_fast_l<F, 16, 1>(sh, job, nmat, nr, max_rows, A, st); return true; }
+  if (L == 8 && cpl == 1) { launch_fast_l<F, 8, 1>(sh, job, nmat, nr, max_rows, A, st); return true; }
   return false;
 }
 
@@ -1190,7 +1202,7 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
 int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_rows, hipStream_t st) {
   if (max_rows <= 0 || nmat <= 0 || sh.O <= 0) return MOE_OK;
   int per, size, vals;
-  if (block_geometry(fmt, &per, &size, &vals)) return run_matvec_blocks(fmt, sh, job, nmat, st);  // GGUF
+  if (block_geometry(fmt, &per, &size, &vals)) return run_matvec_blocks(fmt, sh, job, nmat, max_rows, st);  // GGUF
   if (chunked_ok(fmt, sh)) {
     if (fmt == FMT_Q4 && launch_w24(sh, job, nmat, max_rows, st)) return check_launch("int4 mat-vec (24-byte chunks)");
     if (fmt == FMT_Q4 &&

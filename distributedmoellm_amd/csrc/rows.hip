@@ -47,7 +47,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int kRowsR = 4;  // 16-row blocks of weight rows per wave: 64 rows a wave and row group
+constexpr int kRowsR = 2;            // 16-row blocks of weight rows per wave and row group
+constexpr int kGroupRows = 16 * kRowsR;  // weight rows a wave takes per row group
 
 __device__ __forceinline__ u32x4 wload(const uint8_t* p) {
   return __builtin_nontemporal_load(gptr<u32x4>(p));
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(256) void rows_prep_kernel(const float* x, int ldx,
 
 // ------------------------------------------------------------------ the GEMM
 
-// One wave: weight rows [row0, row0 + 64 * ng) of matrix M (O rows, K columns),
+// One wave: weight rows [row0, row0 + kGroupRows * ng) of matrix M (O rows, K columns),
 // Q quads of input rows (quad q0 + qq, pairs pq + 4 qq + j), all K.
 template <int Q, bool SF16>
 __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int O, int K, int row0, int ng,
@@ -183,7 +184,7 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
   u32x4 sbn[R][SF16 ? 1 : 2], sbc[R][SF16 ? 1 : 2];
   // the weight row of this lane in row block r of row group rg (rows past O read row O - 1)
   auto wrow = [&](int rg, int r) {
-    const int o = row0 + 64 * rg + 16 * r + n;
+    const int o = row0 + kGroupRows * rg + 16 * r + n;
     return (uint32_t)(o < O ? o : O - 1);
   };
   auto issue = [&](int s, auto bc, auto uc) {
@@ -271,7 +272,7 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
       const int p = pq + 4 * qq + j;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int o = row0 + 64 * rg + 16 * r + n;
+        const int o = row0 + kGroupRows * rg + 16 * r + n;
         if (p < p1 && o < O) job.y[(size_t)p * job.ldy + o] = acc[qq][r] * f[qq];
         acc[qq][r] = 0.f;
       }
@@ -281,28 +282,32 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
+  // every issue is unconditional (past the last stage it loads the last stage
+  // again, from L2), so the compiler's wait before a compute leaves the one
+  // stage issued after it in flight; a conditional issue makes it wait for all
+  const int last = nstage - 1;
   issue(0, I0{}, I0{});
   for (int s = 0; s < nstage; s += 4) {
-    if (s + 1 < nstage) issue(s + 1, I1{}, I1{});
+    issue(min(s + 1, last), I1{}, I1{});
     compute(I0{}, I0{});
     finish(s);
     if (s + 1 >= nstage) break;
-    if (s + 2 < nstage) issue(s + 2, I0{}, I2{});
+    issue(min(s + 2, last), I0{}, I2{});
     compute(I1{}, I1{});
     finish(s + 1);
     if (s + 2 >= nstage) break;
-    if (s + 3 < nstage) issue(s + 3, I1{}, I3{});
+    issue(min(s + 3, last), I1{}, I3{});
     compute(I0{}, I2{});
     finish(s + 2);
     if (s + 3 >= nstage) break;
-    if (s + 4 < nstage) issue(s + 4, I0{}, I0{});
+    issue(min(s + 4, last), I0{}, I0{});
     compute(I1{}, I3{});
     finish(s + 3);
   }
 }
 
 // grid.y = expert of the call, grid.x = (quad of its input rows, group of 4
-// waves over its weight rows); each wave takes ng row groups of 64 rows for
+// waves over its weight rows); each wave takes ng row groups of kGroupRows rows for
 // one quad, so the quads of an expert with many rows run side by side
 __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K, int ng, int tiles,
                                                         const int* qbase, const float* fac, const uint8_t* limbs) {
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K,
   const int p0 = job.seg[mat], p1 = job.seg[mat + 1];
   const int quads = gridDim.x / tiles, tile = blockIdx.x % tiles;
   const int wave = tile * 4 + (threadIdx.x >> 6);
-  const int row0 = wave * 64 * ng;
+  const int row0 = wave * kGroupRows * ng;
   if (row0 >= O) return;  // the whole wave
   const MatRef M = resolve(job, mat);
   // one quad a wave (two quads a pass held about 230 VGPRs, one wave a SIMD);
@@ -322,7 +327,7 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K,
       // other arrays give NaN rather than a wrong product
       const int lane = threadIdx.x & 63, pe = min(pq + 4, p1);
       for (int p = pq; p < pe; ++p)
-        for (int o = row0 + lane; o < row0 + 64 * ng && o < O; o += 64)
+        for (int o = row0 + lane; o < row0 + kGroupRows * ng && o < O; o += 64)
           job.y[(size_t)p * job.ldy + o] = __builtin_nanf("");
       continue;
     }
@@ -366,7 +371,7 @@ int run_rows_prep(const float* x, int ldx, const int* xrow, const int* poff, int
 int run_rows_gemm(const MVJob& job, int k, int O, int K, int max_rows, const RowsSpace& ws, const uint8_t* limbs,
                   hipStream_t st) {
   if (k <= 0 || O <= 0 || max_rows <= 0) return MOE_OK;
-  const int groups = (O + 63) / 64;  // row groups of 64 per matrix
+  const int groups = (O + kGroupRows - 1) / kGroupRows;  // row groups per matrix
   const int quads = (max_rows + 3) / 4;
   // one row group a wave: most experts have one quad, and a wave streams its
   // rows at a few GB/s, so the work is spread over as many waves as it allows
