@@ -7,6 +7,7 @@
 #include "../../include/moehip.h"
 #include "common.h"
 #include "blocks.h"
+#include "dqgemm.h"
 #include "dequant.h"
 #include "layer.h"
 #include "matvec.h"
@@ -95,6 +96,10 @@ MOE_API int moe_q4_matmul_t(const float* x, int n, const uint8_t* raw, const voi
   REQUIRE(n >= 0, "moe_q4_matmul_t: n=%d", n);
   if (n == 0) return MOE_OK;
   REQUIRE(x && raw && s && y, "moe_q4_matmul_t: null pointer");
+  if (n >= kDqRows) {  // many rows: widened in registers, f32 MFMA
+    const DqArgs d{x, I, n, raw, s, s_f16, offset ? 0u : 0x88888888u, O, I, gs, y, O};
+    if (dq_mfma_ok(DQ_INT4, d)) return run_dq_mfma(DQ_INT4, d, as_stream(stream));
+  }
   MVShape sh;
   plan_matvec(FMT_Q4, O, I, gs, &sh);
   MVJob j{};
@@ -113,6 +118,10 @@ MOE_API int moe_q8_matmul_t(const float* x, int n, const int8_t* q, const void* 
   REQUIRE(n >= 0, "moe_q8_matmul_t: n=%d", n);
   if (n == 0) return MOE_OK;
   REQUIRE(x && q && s && y, "moe_q8_matmul_t: null pointer");
+  if (n >= kDqRows) {  // many rows: widened in registers, f32 MFMA
+    const DqArgs d{x, I, n, q, s, s_f16, 0u, O, I, gs, y, O};
+    if (dq_mfma_ok(DQ_INT8, d)) return run_dq_mfma(DQ_INT8, d, as_stream(stream));
+  }
   MVShape sh;
   plan_matvec(FMT_Q8, O, I, gs, &sh);
   MVJob j{};
@@ -142,6 +151,11 @@ MOE_API int moe_gguf_matmul_t(const float* x, int n, const uint8_t* raw, int qty
   REQUIRE(n >= 0, "moe_gguf_matmul_t: n=%d", n);
   if (n == 0) return MOE_OK;
   REQUIRE(x && raw && y, "moe_gguf_matmul_t: null pointer");
+  if ((qtype == FMT_Q8_0 || qtype == FMT_Q4_K) && n >= kDqRows) {  // many rows: blocks widened in registers, f32 MFMA
+    const int wf = qtype == FMT_Q8_0 ? DQ_Q8_0 : DQ_Q4_K;
+    const DqArgs d{x, cols, n, raw, nullptr, 1, 0u, O, cols, 32, y, O};
+    if (dq_mfma_ok(wf, d)) return run_dq_mfma(wf, d, as_stream(stream));
+  }
   MVShape sh;
   plan_matvec(qtype, O, cols, blk, &sh);
   MVJob j{};

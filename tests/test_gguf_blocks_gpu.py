@@ -91,3 +91,29 @@ def test_q4_k_m_style_expert(kernels):
     Wd = R.gguf_dequant(e.down.raw, R.Q6_K, I)
     want = R.expert_exact(x, np.concatenate([Wg, Wu], 0).astype(np.float64), Wd.astype(np.float64), I)
     close(e(x), want)
+
+
+@pytest.mark.parametrize("qtype", [R.Q8_0, R.Q4_K], ids=["Q8_0", "Q4_K"])
+@pytest.mark.parametrize("rows", [16, 32, 50])
+@pytest.mark.parametrize("O,cols", [(768, 2048), (2048, 768), (37, 256)])
+def test_many_rows_mfma(kernels, qtype, rows, O, cols):
+    """From 16 rows a Q8_0 / Q4_K product widens each block in registers with
+    the dequant's own f32 operations and runs f32 MFMA: within 1e-5 of the
+    float64 product of the decoded weights."""
+    rng = np.random.default_rng(rows + O + qtype)
+    raw = R.random_blocks(O, cols, qtype, rng)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    close(kernels.gguf_matmul_t(x, raw, qtype, cols), R.gguf_matmul_t(x, raw, qtype, cols))
+
+
+@pytest.mark.parametrize("qtype", [R.Q8_0, R.Q4_K], ids=["Q8_0", "Q4_K"])
+def test_many_rows_mfma_one_hot_exact(kernels, qtype):
+    """Row i of x = e_c: column c of the decoded matrix bit for bit."""
+    rng = np.random.default_rng(40 + qtype)
+    O, cols = 64, 512
+    raw = R.random_blocks(O, cols, qtype, rng)
+    W = R.gguf_dequant(raw, qtype, cols)
+    cs = [0, 1, 31, 32, 33, 63, 64, 127, 128, 200, 255, 256, 300, 383, 384, 511]
+    x = np.zeros((len(cs), cols), np.float32)
+    x[np.arange(len(cs)), cs] = 1.0
+    assert np.array_equal(kernels.gguf_matmul_t(x, raw, qtype, cols), W[:, cs].T)

@@ -346,3 +346,63 @@ def test_q4_w24_one_hot_columns_are_exact(kernels):
         x[0, c] = 1.0
         y = kernels.q4_matmul_t(x, raw, s, gs, False)
         assert np.array_equal(y[0], W[:, c]), f"column {c}"
+
+
+# ---------------------------------------------------------------- many rows: f32 MFMA product
+
+@pytest.mark.parametrize("rows", [16, 33, 64])
+@pytest.mark.parametrize("O,I,gs", [(1536, 2048, 32), (2048, 768, 32), (100, 256, 64), (37, 512, 128)])
+@pytest.mark.parametrize("sdt", [np.float16, np.float32])
+def test_q8_matmul_many_rows(kernels, rows, O, I, gs, sdt):
+    """From 16 rows the int8 product widens q * s in registers and runs f32
+    MFMA (exact weights, f32 sums): within 1e-5 of float64, rows and weight
+    rows past a 16-tile edge included."""
+    rng = np.random.default_rng(rows * 3 + O + I)
+    q = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, (O, I // gs))) / 127).astype(sdt)
+    x = rng.standard_normal((rows, I)).astype(np.float32)
+    close(kernels.q8_matmul_t(x, q, s, gs), R.q8_matmul_t(x, q, s, gs))
+
+
+@pytest.mark.parametrize("rows", [16, 40])
+@pytest.mark.parametrize("offset", [False, True])
+@pytest.mark.parametrize("O,I,gs,sdt", [(1536, 2048, 32, np.float16), (4096, 1536, 32, np.float16),
+                                        (70, 512, 64, np.float32), (48, 320, 32, np.float32)])
+def test_q4_matmul_many_rows(kernels, rows, offset, O, I, gs, sdt):
+    rng = np.random.default_rng(rows + O * 5 + int(offset))
+    raw, s = int4_matrix(rng, O, I, gs, sdt)
+    x = rng.standard_normal((rows, I)).astype(np.float32)
+    close(kernels.q4_matmul_t(x, raw, s, gs, offset), R.q4_matmul_t(x, raw, s, gs, offset))
+
+
+def test_many_rows_one_hot_columns_are_exact(kernels):
+    """Row c of x = e_c: the f32 MFMA product returns column c of the widened
+    matrix bit for bit (int4 and int8), across chunk and group edges."""
+    rng = np.random.default_rng(9)
+    O, I, gs = 80, 256, 32
+    cols = [0, 1, 15, 16, 31, 32, 63, 64, 100, 127, 128, 200, 255, 3, 77, 190, 250]
+    x = np.zeros((len(cols), I), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    raw, s = int4_matrix(rng, O, I, gs)
+    W = R.q4_dequant(raw, s, gs, False)
+    assert np.array_equal(kernels.q4_matmul_t(x, raw, s, gs, False), W[:, cols].T)
+    q = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    s8 = (np.abs(rng.normal(0, 0.02, (O, I // gs))) / 127).astype(np.float16)
+    W8 = R.q8_dequant(q, s8, gs)
+    assert np.array_equal(kernels.q8_matmul_t(x, q, s8, gs), W8[:, cols].T)
+
+
+def test_many_rows_dynamic_range_and_non_finite(kernels):
+    """Rows scaled by 1e20 and 1e-20 stay within 1e-5 (f32 products and sums);
+    a NaN in a row makes that row's outputs NaN and leaves the others."""
+    rng = np.random.default_rng(10)
+    O, I, gs = 256, 512, 32
+    raw, s = int4_matrix(rng, O, I, gs)
+    x = rng.standard_normal((32, I)).astype(np.float32)
+    x[:8] *= 1e20
+    x[8:16] *= 1e-20
+    close(kernels.q4_matmul_t(x, raw, s, gs, False), R.q4_matmul_t(x, raw, s, gs, False))
+    x[20, 100] = np.nan
+    y = kernels.q4_matmul_t(x, raw, s, gs, False)
+    assert np.isnan(y[20]).all()
+    assert np.isfinite(np.delete(y, 20, 0)).all()
