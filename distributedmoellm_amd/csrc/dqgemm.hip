@@ -222,8 +222,10 @@ int launch_dq(const DqArgs& a, hipStream_t st) {
   };
   constexpr Cfg cfgs[] = {{4, 4}, {2, 8}, {2, 4}, {1, 16}, {1, 8}, {1, 4}};
   const int chunks = a.K / (4 * WSlice<WF>::kCols), mtiles = (a.n + 15) / 16, ntiles = (a.O + 15) / 16;
+  // (GGUF chunks are twice as wide: a small GGUF product wants 16 slices)
   int pick;
   if ((long)ntiles * mtiles >= 4096) pick = mtiles >= 4 ? 0 : (mtiles >= 2 ? 2 : 5);
+  else if (WSlice<WF>::kCols == 32) pick = chunks >= 16 ? 3 : (chunks >= 8 ? 4 : 5);
   else pick = mtiles >= 2 ? 2 : (chunks >= 8 ? 4 : 5);
   static const int env = [] {
     const char* e = getenv("MOEHIP_DQ_CFG");  // tuning override: index into cfgs
