@@ -27,10 +27,12 @@
 // 32g + 8j + {0, 2, 4, 6, 1, 3, 5, 7} (the low nibbles of the weight dword j of
 // the group come first, then its high nibbles).
 //
-// Weight loads: lane (j, n) of a wave reads 16 bytes of weight row n at
-// 64 h + 16 j (h = 0, 1) of each 128-byte stage (8 groups); a 4 x 4 dword
-// transpose across the lane rows (v_permlane32_swap / v_permlane16_swap) leaves
-// dword j of group q of row n in register q of lane (j, n), the MFMA B layout.
+// Weight loads: each load instruction reads whole 128-byte lines -- 8 rows x
+// the stage's 128 bytes (8 groups), lane (r8, c8) the 16 bytes of group c8 of
+// row r8 -- and a pass through the wave's own LDS area leaves dword j of
+// group q of row n in register q of lane (j, n), the MFMA B layout. (Lanes
+// reading 16-byte halves of lines across 16 rows, transposed with permlanes,
+// streamed about a fifth slower.)
 // Scale loads: lane (j, n) reads the 8 scales of stage 4b + j of row n, and
 // stage 4b + u takes them from lane (u, n) with ds_bpermute (one load per row
 // and 4 stages instead of 16 lines per load).
@@ -52,20 +54,6 @@ constexpr int kGroupRows = 16 * kRowsR;  // weight rows a wave takes per row gro
 
 __device__ __forceinline__ u32x4 wload(const uint8_t* p) {
   return __builtin_nontemporal_load(gptr<u32x4>(p));
-}
-
-// 4 x 4 dword transpose across the lane rows {n, n + 16, n + 32, n + 48}:
-// on entry lane row j holds dwords 0..3 of group j, on exit register q of lane
-// row j holds dword j of group q
-__device__ __forceinline__ void transpose4(u32x4& v) {
-  const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
-  const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
-  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-  v.x = c[0];
-  v.y = c[1];
-  v.z = d[0];
-  v.w = d[1];
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -169,7 +157,8 @@ __global__ __launch_bounds__(256) void rows_prep_kernel(const float* x, int ldx,
 // Q quads of input rows (quad q0 + qq, pairs pq + 4 qq + j), all K.
 template <int Q, bool SF16>
 __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int O, int K, int row0, int ng,
-                                          const uint8_t* limbs, int q0, int pq, int p1, const float* fac) {
+                                          const uint8_t* limbs, int q0, int pq, int p1, const float* fac,
+                                          uint32_t* tw) {
   constexpr int R = kRowsR;
   constexpr uint32_t SB = SF16 ? 16u : 32u;  // scale bytes of a row per stage
   const int lane = threadIdx.x & 63, n = lane & 15, j = lane >> 4;
@@ -187,14 +176,20 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
     const int o = row0 + kGroupRows * rg + 16 * r + n;
     return (uint32_t)(o < O ? o : O - 1);
   };
+  // whole 128-byte lines: lane (r8, c8) = (lane / 8, lane % 8) reads group c8
+  // of the stage (16 bytes) of rows r8 and r8 + 8 of each 16-row block
+  const int r8 = lane >> 3, c8 = lane & 7;
+  auto lrow = [&](int rg, int r, int h) {
+    const int o = row0 + kGroupRows * rg + 16 * r + 8 * h + r8;
+    return (uint32_t)(o < O ? o : O - 1);
+  };
   auto issue = [&](int s, auto bc, auto uc) {
     constexpr int B = decltype(bc)::value, U = decltype(uc)::value;  // U = s % 4
     const int rg = s / T, t = s - rg * T;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint8_t* p = W + (wrow(rg, r) * rb + 128u * t + 16u * j);
-      wb[B][r][0] = wload(p);
-      wb[B][r][1] = wload(p + 64);
+      wb[B][r][0] = wload(W + (lrow(rg, r, 0) * rb + 128u * t + 16u * c8));
+      wb[B][r][1] = wload(W + (lrow(rg, r, 1) * rb + 128u * t + 16u * c8));
     }
     if constexpr (U == 0) {  // scales of stages s .. s + 3: stage s + j in lane (j, n)
       const int sj = s + j < nstage ? s + j : nstage - 1;
@@ -233,9 +228,19 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
     const int src = (U * 16 + n) * 4;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      u32x4 w0 = wb[B][r][0], w1 = wb[B][r][1];
-      transpose4(w0);
-      transpose4(w1);
+      // to the MFMA B layout through this wave's LDS area: dword d of group
+      // c8 of row m goes to word 36 m + 8 d + c8 (rows 144 bytes apart: the
+      // writes of a row's 8 lanes spread over the banks), and lane (n, j)
+      // reads words 36 n + 8 j .. + 8: dword j of groups 0..7 of row n
+      uint32_t* const area = tw + r * (16 * 36);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) area[36 * (r8 + 8 * h) + 8 * d + c8] = wb[B][r][h][d];
+      __builtin_amdgcn_wave_barrier();
+      const u32x4 w0 = *reinterpret_cast<const u32x4*>(area + 36 * n + 8 * j);
+      const u32x4 w1 = *reinterpret_cast<const u32x4*>(area + 36 * n + 8 * j + 4);
+      __builtin_amdgcn_wave_barrier();
       const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
       uint32_t sw[SF16 ? 4 : 8];
 #pragma unroll
@@ -311,6 +316,7 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
 // one quad, so the quads of an expert with many rows run side by side
 __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K, int ng, int tiles,
                                                         const int* qbase, const float* fac, const uint8_t* limbs) {
+  __shared__ __attribute__((aligned(16))) uint32_t tw[4][kRowsR * 16 * 36];  // each wave's weight transpose area
   const int mat = blockIdx.y;
   const int p0 = job.seg[mat], p1 = job.seg[mat + 1];
   const int quads = gridDim.x / tiles, tile = blockIdx.x % tiles;
@@ -332,8 +338,9 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K,
       continue;
     }
     const int q = qbase[mat] + qp;
-    if (M.s_f16) rows_wave<1, true>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac);
-    else rows_wave<1, false>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac);
+    uint32_t* const area = tw[threadIdx.x >> 6];
+    if (M.s_f16) rows_wave<1, true>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac, area);
+    else rows_wave<1, false>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac, area);
   }
 }
 
