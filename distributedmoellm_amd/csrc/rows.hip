@@ -158,8 +158,10 @@ __global__ __launch_bounds__(256) void rows_prep_kernel(const float* x, int ldx,
 template <int Q, bool SF16>
 __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int O, int K, int row0, int ng,
                                           const uint8_t* limbs, int q0, int pq, int p1, const float* fac,
-                                          uint32_t* tw) {
+                                          uint32_t* tw, u32x4 (*act)[4][64]) {
+  static_assert(Q == 1, "the workgroup shares one quad's limbs");
   constexpr int R = kRowsR;
+  const int wv = threadIdx.x >> 6;
   constexpr uint32_t SB = SF16 ? 16u : 32u;  // scale bytes of a row per stage
   const int lane = threadIdx.x & 63, n = lane & 15, j = lane >> 4;
   const uint32_t rb = (uint32_t)K / 2, G = (uint32_t)K / 32;
@@ -169,7 +171,7 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
   const uint8_t* const S = static_cast<const uint8_t*>(M.s);
   const uint8_t* const A = limbs + (size_t)q0 * (K / 64) * 1024 + 16 * lane;
 
-  u32x4 wb[2][R][2], ab[2][Q][4];
+  u32x4 wb[2][R][2], ap[2];
   u32x4 sbn[R][SF16 ? 1 : 2], sbc[R][SF16 ? 1 : 2];
   // the weight row of this lane in row block r of row group rg (rows past O read row O - 1)
   auto wrow = [&](int rg, int r) {
@@ -183,9 +185,14 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
     const int o = row0 + kGroupRows * rg + 16 * r + 8 * h + r8;
     return (uint32_t)(o < O ? o : O - 1);
   };
+  // The 4 waves of a workgroup take the same quad: wave wv loads the stage's
+  // limb block wv (1 KB) and puts it in the workgroup's LDS slot s % 2; each
+  // wave reads all 4 from there after the stage's barrier. The block load is
+  // issued first, so that waiting for it leaves the stage's weights in flight.
   auto issue = [&](int s, auto bc, auto uc) {
     constexpr int B = decltype(bc)::value, U = decltype(uc)::value;  // U = s % 4
     const int rg = s / T, t = s - rg * T;
+    ap[B] = *gptr<u32x4>(A + ((size_t)(4 * t + wv)) * 1024);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       wb[B][r][0] = wload(W + (lrow(rg, r, 0) * rb + 128u * t + 16u * c8));
@@ -201,10 +208,10 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
         for (int h = 0; h < (SF16 ? 1 : 2); ++h) sbn[r][h] = *gptr<u32x4>(p + 16 * h);
       }
     }
-#pragma unroll
-    for (int qq = 0; qq < Q; ++qq)
-#pragma unroll
-      for (int h = 0; h < 4; ++h) ab[B][qq][h] = *gptr<u32x4>(A + ((size_t)qq * (K / 64) + 4 * t + h) * 1024);
+  };
+  auto put = [&](auto bc) {  // this wave's limb block of the stage in slot B
+    constexpr int B = decltype(bc)::value;
+    act[B][wv][lane] = ap[B];
   };
   float acc[Q][R];
 #pragma unroll
@@ -219,6 +226,11 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
   }
   auto compute = [&](auto bc, auto uc) {
     constexpr int B = decltype(bc)::value, U = decltype(uc)::value;
+    __syncthreads();  // every wave's limb block of this stage is in slot B; slot B ^ 1 is free
+    u32x4 ab[Q][4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) ab[0][h] = act[B][h][lane];
+    put(std::integral_constant<int, B ^ 1>{});  // the next stage's block (issued before this compute)
     if constexpr (U == 0) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -254,7 +266,7 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
         for (int g = 0; g < 8; ++g) {
           const uint32_t wd = w[g] ^ flip;
           const long b = (long)(((uint64_t)(wd & 0xF0F0F0F0u) << 32) | ((wd << 4) & 0xF0F0F0F0u));
-          const u32x4 a2 = ab[B][qq][g >> 1];
+          const u32x4 a2 = ab[qq][g >> 1];
           const long a = (g & 1) ? (long)(((uint64_t)a2.w << 32) | a2.z) : (long)(((uint64_t)a2.y << 32) | a2.x);
           tm[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
         }
@@ -292,6 +304,8 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
   // stage issued after it in flight; a conditional issue makes it wait for all
   const int last = nstage - 1;
   issue(0, I0{}, I0{});
+  __syncthreads();  // a previous quad's last stage may still be read from slot 0
+  put(I0{});
   for (int s = 0; s < nstage; s += 4) {
     issue(min(s + 1, last), I1{}, I1{});
     compute(I0{}, I0{});
@@ -317,12 +331,14 @@ __device__ __forceinline__ void rows_wave(const MVJob& job, const MatRef& M, int
 __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K, int ng, int tiles,
                                                         const int* qbase, const float* fac, const uint8_t* limbs) {
   __shared__ __attribute__((aligned(16))) uint32_t tw[4][kRowsR * 16 * 36];  // each wave's weight transpose area
+  __shared__ u32x4 act[2][4][64];  // the quad's limb blocks of two stages
   const int mat = blockIdx.y;
   const int p0 = job.seg[mat], p1 = job.seg[mat + 1];
   const int quads = gridDim.x / tiles, tile = blockIdx.x % tiles;
   const int wave = tile * 4 + (threadIdx.x >> 6);
+  // a wave past the last row still runs the stage loop (its barriers): it
+  // reads the last row and stores nothing
   const int row0 = wave * kGroupRows * ng;
-  if (row0 >= O) return;  // the whole wave
   const MatRef M = resolve(job, mat);
   // one quad a wave (two quads a pass held about 230 VGPRs, one wave a SIMD);
   // quads past the grid's (a max_rows below the true count) loop here
@@ -339,8 +355,8 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K,
     }
     const int q = qbase[mat] + qp;
     uint32_t* const area = tw[threadIdx.x >> 6];
-    if (M.s_f16) rows_wave<1, true>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac, area);
-    else rows_wave<1, false>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac, area);
+    if (M.s_f16) rows_wave<1, true>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac, area, act);
+    else rows_wave<1, false>(job, M, O, K, row0, ng, limbs, q, pq, p1, fac, area, act);
   }
 }
 
