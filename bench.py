@@ -798,14 +798,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--extras", action="store_true",
                     help="also run the group-64 int8/float decode, GGUF, wire and residency measurements "
-                         "(each has its own --only part; kept out of the default run so that the default "
-                         "command's kernel trace holds only the headline launches)")
+                         "(each has its own --only part; kept out of the default run to keep it short)")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--batches", default="1,8,32", help="token batches of the 235B-shaped stack decode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay figure of the stack decode "
                                                             "(for counter runs)")
-    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, decode_i8, gguf, wire, residency, prefill, copy "
+    ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, stack, int8, gguf_c3, prefill, decode_i8, gguf, wire, "
+                                                "residency, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
