@@ -7,7 +7,8 @@
 namespace moe {
 
 // Whether the rows GEMM takes a layer of this shape: both matrices' rows are
-// whole 256-column stages (H and I multiples of 256) and the group size is 32.
+// whole 256-column stages (H and I multiples of 256, at most 16384) and the
+// group size is 32.
 bool rows_gemm_ok(int H, int I, int gs);
 
 // Workspace bytes the rows GEMM adds to the layer call for P pairs.
@@ -22,8 +23,9 @@ struct RowsSpace {
 };
 RowsSpace rows_layout(void* base, int P, int H, int I);
 
-// Activation limbs of every pair: which = 0 reads x[xrow[p]] (H values), which
-// = 1 reads silu(h[p, :I]) * h[p, I:] (I values).
+// Activation limbs of every pair: half = 0 reads x[xrow[p]] (K values), half > 0
+// reads silu(x[p, :K]) * x[p, half:half + K]. poff ascends from poff[0] = 0 to
+// poff[k] = P.
 int run_rows_prep(const float* x, int ldx, const int* xrow, const int* poff, int k, int P, int K, int half,
                   const RowsSpace& ws, uint8_t* limbs, hipStream_t st);
 // y[p] = a(p) @ W_m.T for every expert m of the job (its gate|up matrix for

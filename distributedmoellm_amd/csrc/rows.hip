@@ -46,11 +46,13 @@
 namespace moe {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
 constexpr int kRowsR = 2;            // 16-row blocks of weight rows per wave and row group
 constexpr int kGroupRows = 16 * kRowsR;  // weight rows a wave takes per row group
+constexpr int kRowsMaxK = 16384;         // longest row the limb kernel holds in registers (8 chunks a thread)
 
 __device__ __forceinline__ u32x4 wload(const uint8_t* p) {
   return __builtin_nontemporal_load(gptr<u32x4>(p));
@@ -78,63 +80,112 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 
 // ------------------------------------------------------------------ activation limbs
 
-// One block per pair p: its expert m (poff ascending), the expert's first
-// quad (the ceil(n / 4) of the experts before it), the row's scale 2^sigma, and
-// its limbs into slot i % 4 of quad qbase[m] + i / 4, i = p - poff[m].
+// One block per pair p: its expert m, the expert's first quad (the ceil(n / 4)
+// of the experts before it), the row's scale 2^sigma, and its limbs into slot
+// i % 4 of quad qbase[m] + i / 4, i = p - poff[m].
+//  * The row is loaded once, first, into registers: chunk c of thread t holds
+//    columns 8 (t + 256 c) .. 8 (t + 256 c) + 7, NC chunks a thread (K <= 2048 NC).
+//  * poff is ascending from poff[0] = 0, so expert e lies wholly before p
+//    exactly when poff[e + 1] <= p: m is the count of such experts, poff[m] the
+//    sum of their rows and qbase[m] the sum of their quads -- one pass of
+//    independent loads in place of a search of dependent ones.
+template <int NC, bool V4>
 __global__ __launch_bounds__(256) void rows_prep_kernel(const float* x, int ldx, const int* xrow, const int* poff,
-                                                        int k, int P, int K, int half, int* qbase, float* fac,
+                                                        int k, int K, int half, int* qbase, float* fac,
                                                         uint8_t* limbs) {
   __shared__ float red[2][4];
-  __shared__ int qred[4];
+  __shared__ int ired[3][4];
   const int p = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  int lo = 0, hi = k;  // poff[lo] <= p < poff[hi]
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (poff[mid] <= p) lo = mid;
-    else hi = mid;
-  }
-  const int m = lo, i = p - poff[m];
-  int q = 0;
-  for (int e = t; e < m; e += 256) q += (poff[e + 1] - poff[e] + 3) >> 2;
-  q = wave_sum_i(q);
   const float* row = x + (size_t)(xrow ? xrow[p] : p) * ldx;
-  auto value = [&](int c) { return half > 0 ? silu(row[c]) * row[half + c] : row[c]; };
+  const int nch = K / 8;
+  auto load8 = [&](const float* src, float* d) {
+    if constexpr (V4) {
+      const f32x4 a = gptr<f32x4>(src)[0], b = gptr<f32x4>(src)[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d[e] = a[e];
+        d[4 + e] = b[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = src[e];
+    }
+  };
+  float v[NC][8];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int cb = t + 256 * c;
+    if (cb < nch) {
+      load8(row + 8 * cb, v[c]);
+      if (half > 0) {
+        float u[8];
+        load8(row + half + 8 * cb, u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = silu(v[c][e]) * u[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[c][e] = 0.f;
+    }
+  }
+  int m = 0, q = 0, before = 0;
+  for (int e = t; e < k; e += 256) {
+    const int a = poff[e], b = poff[e + 1];
+    if (b <= p) {
+      ++m;
+      q += (b - a + 3) >> 2;
+      before += b - a;
+    }
+  }
   // the largest |v|; z is 0, or NaN when a value is not finite (fmaxf drops NaN)
   float mx = 0.f, z = 0.f;
-  for (int c = t; c < K; c += 256) {
-    const float v = value(c);
-    mx = fmaxf(mx, fabsf(v));
-    z += v - v;
-  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      mx = fmaxf(mx, fabsf(v[c][e]));
+      z += v[c][e] - v[c][e];
+    }
   mx = wave_max_f(mx);
   z = wave_sum_f(z);
+  m = wave_sum_i(m);
+  q = wave_sum_i(q);
+  before = wave_sum_i(before);
   if (lane == 0) {
     red[0][wv] = mx;
     red[1][wv] = z;
-    qred[wv] = q;
+    ired[0][wv] = m;
+    ired[1][wv] = q;
+    ired[2][wv] = before;
   }
   __syncthreads();
   mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
   z = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-  q = (qred[0] + qred[1]) + (qred[2] + qred[3]);
+  m = (ired[0][0] + ired[0][1]) + (ired[0][2] + ired[0][3]);
+  q = (ired[1][0] + ired[1][1]) + (ired[1][2] + ired[1][3]);
+  before = (ired[2][0] + ired[2][1]) + (ired[2][2] + ired[2][3]);
+  const int i = p - before;
   if (i == 0 && t == 0) qbase[m] = q;
   const int quad = q + (i >> 2), slot = i & 3;
   const int sigma = 30 - (mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : 0);
   if (t == 0) fac[p] = __builtin_ldexpf(0.0625f, -sigma) + z;
   const int G2 = K / 64;
   uint8_t* blk = limbs + (size_t)quad * G2 * 1024;
-  // (group g, K slot j) per thread: 8 values at 32 g + 8 j + {0, 2, 4, 6, 1, 3, 5, 7}
-  for (int cb = t; cb < K / 8; cb += 256) {
+  // chunk cb is (group g, K slot j) = (cb / 4, cb % 4): its 8 values go out in
+  // the column order 32 g + 8 j + {0, 2, 4, 6, 1, 3, 5, 7}
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int cb = t + 256 * c;
+    if (cb >= nch) continue;
     const int g = cb >> 2, j = cb & 3;
-    const int c0 = 32 * g + 8 * j;
     uint32_t u[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int col = c0 + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
       // |v| 2^sigma < 2^30 for finite values; the clamp keeps Inf and NaN defined
-      const float v = fminf(fmaxf(__builtin_rintf(__builtin_ldexpf(value(col), sigma)), -1073741824.0f),
+      const float r = fminf(fmaxf(__builtin_rintf(__builtin_ldexpf(v[c][e < 4 ? 2 * e : 2 * (e - 4) + 1], sigma)),
+                                  -1073741824.0f),
                             1073741824.0f);
-      u[e] = (uint32_t)(int)v + 0x80808080u;  // bytes minus 128 are the balanced digits
+      u[e] = (uint32_t)(int)r + 0x80808080u;  // bytes minus 128 are the balanced digits
     }
 #pragma unroll
     for (int L = 0; L < 4; ++L) {
@@ -362,7 +413,9 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(MVJob job, int O, int K,
 
 // ------------------------------------------------------------------ host side
 
-bool rows_gemm_ok(int H, int I, int gs) { return gs == 32 && H % 256 == 0 && I % 256 == 0; }
+bool rows_gemm_ok(int H, int I, int gs) {
+  return gs == 32 && H % 256 == 0 && I % 256 == 0 && H <= kRowsMaxK && I <= kRowsMaxK;
+}
 
 RowsSpace rows_layout(void* base, int P, int H, int I) {
   RowsSpace w{};
@@ -386,8 +439,21 @@ size_t rows_workspace(int P, int H, int I) { return rows_layout(nullptr, P, H, I
 int run_rows_prep(const float* x, int ldx, const int* xrow, const int* poff, int k, int P, int K, int half,
                   const RowsSpace& ws, uint8_t* limbs, hipStream_t st) {
   if (P <= 0 || k <= 0) return MOE_OK;
-  hipLaunchKernelGGL(rows_prep_kernel, dim3(P), dim3(256), 0, st, x, ldx, xrow, poff, k, P, K, half, ws.qbase,
-                     ws.fac, limbs);
+  const bool v4 = aligned(x, 16) && ldx % 4 == 0 && half % 4 == 0;
+  auto go = [&](auto nc) {
+    constexpr int NC = decltype(nc)::value;
+    if (v4)
+      hipLaunchKernelGGL((rows_prep_kernel<NC, true>), dim3(P), dim3(256), 0, st, x, ldx, xrow, poff, k, K, half,
+                         ws.qbase, ws.fac, limbs);
+    else
+      hipLaunchKernelGGL((rows_prep_kernel<NC, false>), dim3(P), dim3(256), 0, st, x, ldx, xrow, poff, k, K, half,
+                         ws.qbase, ws.fac, limbs);
+  };
+  if (K <= 2048) go(std::integral_constant<int, 1>{});
+  else if (K <= 4096) go(std::integral_constant<int, 2>{});
+  else if (K <= 8192) go(std::integral_constant<int, 4>{});
+  else if (K <= kRowsMaxK) go(std::integral_constant<int, 8>{});
+  else return set_error(MOE_EUNSUPPORTED, "multi-row int4 GEMM: rows of %d values", K);
   return check_launch("activation limbs");
 }
 

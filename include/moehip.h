@@ -134,7 +134,8 @@ size_t moe_q4_layer_workspace(int P, int H, int I);
 
 /* out[r] += sum over pairs p of row r of pw[p] * expert(x[r]), for k experts
  * given as table[eidx[m]] (eidx NULL: table[m]) with pairs poff[m]..poff[m+1]
- * (input rows prow[p], gate weights pw[p]). Rows touched: rrow[0..nr), whose
+ * (poff ascending from poff[0] = 0 to poff[k] = P; input rows prow[p], gate
+ * weights pw[p]). Rows touched: rrow[0..nr), whose
  * pairs are rpair[rptr[i]..rptr[i+1]] in ascending order; each row's sum is
  * formed in a fixed order (as moe_combine) and then added to out, as the
  * reference does.
