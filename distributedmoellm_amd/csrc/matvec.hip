@@ -1009,6 +1009,20 @@ int row_slices(int max_rows, int NR, long waves) {
   return (int)(z > 65535 ? 65535 : z);
 }
 
+// Stages a wave must stream for the down mat-vec to take its LDS ring: a
+// launch of a few experts gives each resident wave only a few stages, and
+// then the register path is faster (8 experts x [4096 x 1536]: 13.8 against
+// 17.1 us; at 384 experts each wave streams 32 stages and the ring wins).
+// MOEHIP_MV_RING_MIN=n overrides it (a measurement switch).
+static int ring_min_stages() {
+  static const int v = [] {
+    const char* e = getenv("MOEHIP_MV_RING_MIN");
+    const int n = e ? atoi(e) : 0;
+    return n >= 1 && n <= 4096 ? n : 8;
+  }();
+  return v;
+}
+
 template <class F, int L, int CPL>
 static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr, int max_rows, int A, hipStream_t st) {
   auto go = [&](auto kernel, int G, int NR) {
@@ -1160,7 +1174,6 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
     const long slots = ring_off ? 0 : ring_slots(reinterpret_cast<const void*>(kernel), 256, ring_lds);
     if (slots > 0) {
       stride = ring_stride;
-      lds = ring_lds;
       static const int rounds = [] {
         const char* e = getenv("MOEHIP_MV_RING_ROUNDS");  // tuning override
         const int v = e ? atoi(e) : 0;
@@ -1171,7 +1184,12 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
       wpm = wpm < 1 ? 1 : (wpm > spm ? spm : wpm);
       ng = (int)((spm + wpm - 1) / wpm);
       wave_rows = ng * 2 * rpp;
+      if (ng < ring_min_stages()) stride = 0;
+    }
+    if (stride > 0) {
+      lds = ring_lds;
     } else {
+      lds = 0;
       const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));
       const int ng_max = job.half_in > 0 ? 32 : 16;
       ng = (int)(groups / 2048);

@@ -348,6 +348,37 @@ def test_q4_w24_one_hot_columns_are_exact(kernels):
         assert np.array_equal(y[0], W[:, c]), f"column {c}"
 
 
+@pytest.mark.parametrize("H,I,gs,sdt,n", [(4096, 1536, 32, np.float16, 64), (2048, 768, 16, np.float32, 256),
+                                          (960, 768, 64, np.float16, 256), (2048, 384, 32, np.float16, 384)])
+def test_q4_w24_ring_many_experts(kernels, H, I, gs, sdt, n):
+    """The down sweep of moe_q4_experts_matvec over n experts, one row each
+    (SiLU(gate) * up on load): with this many matrices every resident wave
+    streams 8 or more stages, which takes the LDS ring (a single matrix or a
+    few take the register path, covered above). One expert's row holds a NaN
+    and gives NaN outputs; the rest are within 1e-5 of float64."""
+    from distributedmoellm_amd import _lib
+    from distributedmoellm_amd import experts as X
+    rng = np.random.default_rng(H + I + gs + n)
+    ex = [X.synthetic_expert(H, I, "int4", gs, rng, scale_dtype=sdt) for _ in range(n)]
+    h = rng.standard_normal((n, 2 * I)).astype(np.float32)
+    h[n // 2, 5] = np.nan
+    meta = kernels.LayerMeta([kernels.q4_expert_ptrs(e) for e in ex], [np.array([i], np.int32) for i in range(n)],
+                             [np.ones(1, np.float32)] * n)
+    dev = torch.device("cuda")
+    hd = torch.from_numpy(h).to(dev)
+    y = torch.empty((n, H), dtype=torch.float32, device=dev)
+    _lib.call("moe_q4_experts_matvec", hd.data_ptr(), 2 * I, None, meta.table, None, meta.k, meta.poff, 1,
+              H, I, gs, 1, y.data_ptr(), H, kernels.stream_handle())
+    got = y.cpu().numpy()
+    h64 = h.astype(np.float64)
+    a = R.silu(h64[:, :I]) * h64[:, I:]
+    want = np.stack([R.matmul_t_exact(a[i:i + 1], R.q4_dequant64(e.down.raw, e.down.s, gs, False))[0]
+                     for i, e in enumerate(ex)])
+    assert np.isnan(got[n // 2]).all()
+    keep = np.arange(n) != n // 2
+    close(got[keep], want[keep])
+
+
 # ---------------------------------------------------------------- many rows: f32 MFMA product
 
 @pytest.mark.parametrize("rows", [16, 33, 64])
