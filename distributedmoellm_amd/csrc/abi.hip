@@ -462,8 +462,8 @@ static PrefillWs prefill_layout(void* base, int T, int E, int k, int H, int I) {
   w.experts = (int*)take((size_t)E * 4);
   w.offsets = (int*)take(((size_t)E + 1) * 4);
   w.n_used = (int*)take(4);
-  w.xs = (_Float16*)take(P * H * 2);
-  w.xf = (float*)take(P * 4);
+  w.xs = (_Float16*)take((size_t)T * H * 2);  // the tokens' f16 rows, written by the routing
+  w.xf = (float*)take((size_t)T * 4);
   w.act = (_Float16*)take(P * I * 2);
   w.af = (float*)take(P * (I / 16) * 4);
   w.y = (float*)take(P * H * 4);
@@ -471,18 +471,17 @@ static PrefillWs prefill_layout(void* base, int T, int E, int k, int H, int I) {
   return w;
 }
 
-// The expert FFN of grouped rows on the MFMA GEMM: xs / xf take the gathered
-// f16 rows and their factors, act / af silu(gate) * up and its factors (per row
-// and 16 columns); y [P, H] f32.
-static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nexp, const int* eoff, const int* rows,
-                       int P, int H, int I, int gs, _Float16* xs, float* xf, _Float16* act, float* af, float* y,
-                       int ldy, hipStream_t st) {
-  int rc = run_gather_f16(x, ldx, rows, P, H, xs, xf, st);
-  if (rc) return rc;
+// The expert FFN of grouped rows on the MFMA GEMM, from f16 rows xs with
+// factors xf: grouped row q is xs[xrows[q]] (xrows null: xs[q]). act / af take
+// silu(gate) * up and its factors (per row and 16 columns); y [P, H] f32.
+static int grouped_ffn_f16(const _Float16* xs, const float* xf, const int* xrows, const ExpertDesc* table, int nexp,
+                           const int* eoff, int P, int H, int I, int gs, _Float16* act, float* af, float* y, int ldy,
+                           hipStream_t st) {
   GemmArgs g{};
   g.A = xs;
   g.lda = H;
   g.xfac = xf;
+  g.rows = xrows;
   g.eoff = eoff;
   g.table = table;
   g.which = 0;
@@ -493,8 +492,7 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   g.ldact = I;
   g.act_fac = af;
   g.ldaf_out = I / 16;
-  rc = run_gemm(MODE_GATE_UP, g, nexp, st);
-  if (rc) return rc;
+  if (int rc = run_gemm(MODE_GATE_UP, g, nexp, st)) return rc;
   GemmArgs d{};
   d.A = act;
   d.lda = I;
@@ -508,7 +506,17 @@ static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nex
   d.gs = gs;
   d.Y = y;
   d.ldy = ldy;
+  (void)P;
   return run_gemm(MODE_DOWN, d, nexp, st);
+}
+
+// The same from f32 rows x[rows[q]], gathered into xs / xf (f16) first.
+static int grouped_ffn(const float* x, int ldx, const ExpertDesc* table, int nexp, const int* eoff, const int* rows,
+                       int P, int H, int I, int gs, _Float16* xs, float* xf, _Float16* act, float* af, float* y,
+                       int ldy, hipStream_t st) {
+  int rc = run_gather_f16(x, ldx, rows, P, H, xs, xf, st);
+  if (rc) return rc;
+  return grouped_ffn_f16(xs, xf, nullptr, table, nexp, eoff, P, H, I, gs, act, af, y, ldy, st);
 }
 
 // shapes the MFMA tiles do not take are unsupported (not invalid for the format)
@@ -633,10 +641,10 @@ MOE_API int moe_prefill_layer(const float* x, int ldx, const float* router, int 
       nz = router_slices(n, E, H);
       rc = run_router_partials(xp, ldx, router, n, E, H, nz, w.logits, st);
     }
-    if (!rc) rc = run_route(w.logits, nz, n, E, k, normalize, w.idx, w.w, st);
+    // the routing also writes each token's f16 row; grouped row q reads its token's, rows[q]
+    if (!rc) rc = run_route(w.logits, nz, n, E, k, normalize, w.idx, w.w, st, xp, ldx, H, w.xs, w.xf);
     if (!rc) rc = run_group(w.idx, w.w, n, k, E, w.eoff, w.rows, w.wts, w.pos, nullptr, nullptr, nullptr, st);
-    if (!rc)
-      rc = grouped_ffn(xp, ldx, tab, E, w.eoff, w.rows, n * k, H, I, gs, w.xs, w.xf, w.act, w.af, w.y, H, st);
+    if (!rc) rc = grouped_ffn_f16(w.xs, w.xf, w.rows, tab, E, w.eoff, n * k, H, I, gs, w.act, w.af, w.y, H, st);
     if (!rc) rc = run_token_combine(w.y, H, w.pos, w.wts, n, k, H, out + (size_t)t0 * ldo, ldo, st);
     if (rc) return rc;
   }

@@ -11,15 +11,15 @@ struct GemmArgs {
   // a power of two (GATE_UP: xfac[m] undoes it; DOWN: afac[m * ldaf + c]
   // undoes it for 16-column piece c), or
   // f32 rows X (PLAIN, rows32) scaled per row while staged.
-  const _Float16* A;  // [P, K] (rows32 == 0)
+  const _Float16* A;  // [P, K] (rows32 == 0); GATE_UP with `rows`: [*, lda] rows taken through `rows`
   int lda;
-  const float* xfac;  // GATE_UP
+  const float* xfac;  // GATE_UP (with `rows`: per row of A)
   const float* afac;  // DOWN
   int ldaf;
   int rows32;          // activations are f32 rows of X gathered through `rows` (PLAIN only)
   const float* X;      // [*, ldx] f32
   int ldx;
-  const int* rows;     // row of X for each grouped row (null: the grouped row itself)
+  const int* rows;     // row of X (rows32) or of A (GATE_UP) for each grouped row (null: the grouped row itself)
   const int* eoff;           // [nexp + 1] rows of expert e: eoff[e] .. eoff[e+1]
   const ExpertDesc* table;   // expert e's matrices; null: `single` with rows 0 .. single_rows
   ExpertDesc single;
@@ -54,7 +54,10 @@ int run_router_mfma(const float* x, int ldx, const float* R, int T, int E, int H
 // MFMA when it applies, else split K: scratch router_slices(T, E, H) * T * E floats (null: one slice)
 int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int H, float* logits, float* scratch,
                       hipStream_t st);
-int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st);
+// xs (optional): token t's row x[t] (H values) also goes out as its f16 copy
+// xs[t] (as run_gather_f16) with factor xf[t]
+int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st,
+              const float* x = nullptr, int ldx = 0, int H = 0, _Float16* xs = nullptr, float* xf = nullptr);
 // experts / offsets / n_used may be null (not produced)
 int run_group(const int* idx, const float* w, int T, int k, int E, int* eoff, int* rows, float* wts, int* pos,
               int* experts, int* offsets, int* n_used, hipStream_t st);

@@ -227,6 +227,82 @@ __device__ __noinline__ float pairwise_sum(const float* a, int n) {
 // numpy's argsort puts NaN last. key = p, or -1 for NaN (p >= 0 otherwise).
 __device__ __forceinline__ float pick_key(float p) { return p == p ? p : -1.f; }
 
+// ------------------------------------------------------------------ gather
+
+// 2^(t - e) for m = f * 2^e, f in [0.5, 1): m times it lands in [2^(t-1), 2^t);
+// 1 for m = 0 or non-finite m
+__device__ __forceinline__ float pow2_into(float m, int t) {
+  if (!(m > 0.f && m < INFINITY)) return 1.f;
+  return ldexpf(1.f, t - __builtin_amdgcn_frexp_expf(m));
+}
+
+// One wave's f16 copy of a row of K floats: dst = f16(src * 2^a) with each 8
+// columns in MFMA order, the power chosen from the row's largest |value| (so no
+// value overflows f16); *fac = 2^-a. Up to 2048 values stay in registers
+// between the load (issued early, so its latency overlaps other work) and the
+// store; longer rows read their tail twice.
+struct HeldRow {
+  static constexpr int kHeld = 4;  // 8-column groups a lane holds
+  float4 v[kHeld][2];
+
+  __device__ __forceinline__ void load(const float* src, int K, int lane) {
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) {
+      const int c = 8 * lane + 512 * k;
+      if (c < K) {
+        v[k][0] = *reinterpret_cast<const float4*>(src + c);
+        v[k][1] = *reinterpret_cast<const float4*>(src + c + 4);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store_f16(const float* src, int K, _Float16* dst, float* fac, int lane) const {
+    float m = 0.f;
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) {
+      if (8 * lane + 512 * k < K) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k][h].x), fabsf(v[k][h].y)), fmaxf(fabsf(v[k][h].z), fabsf(v[k][h].w))));
+      }
+    }
+    for (int c = 8 * lane + 512 * kHeld; c < K; c += 512) {
+      const float4 lo = *reinterpret_cast<const float4*>(src + c), hi = *reinterpret_cast<const float4*>(src + c + 4);
+      m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
+                         fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w)))));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float f = pow2_into(m, 14);
+    auto put = [&](int c, float4 lo, float4 hi) {
+      const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      half8 h;
+#pragma unroll
+      for (int p = 0; p < 8; ++p) h[p] = (_Float16)(w[(p & 1) * 4 + (p >> 1)] * f);
+      *reinterpret_cast<half8*>(dst + c) = h;
+    };
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) {
+      const int c = 8 * lane + 512 * k;
+      if (c < K) put(c, v[k][0], v[k][1]);
+    }
+    for (int c = 8 * lane + 512 * kHeld; c < K; c += 512)
+      put(c, *reinterpret_cast<const float4*>(src + c), *reinterpret_cast<const float4*>(src + c + 4));
+    if (lane == 0) *fac = 1.f / f;
+  }
+};
+
+// Xs[q, :] = the f16 copy of x[rows[q], :], fac[q] its factor. One wave a row.
+__global__ __launch_bounds__(256) void gather_f16_kernel(const float* x, int ldx, const int* rows, int P, int K,
+                                                         _Float16* Xs, int ldxs, float* fac) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (q >= P) return;
+  const float* src = x + (size_t)(rows ? rows[q] : q) * ldx;
+  HeldRow row;
+  row.load(src, K, lane);
+  row.store_f16(src, K, Xs + (size_t)q * ldxs, fac + q, lane);
+}
+
 // One wave per token: softmax over the E logits (f32: x - max, exp, / sum),
 // then k picks, each the best (key, id) after the previous pick in that order
 // (no per-expert state, so E and k are not bounded), then w / sum(w) when
@@ -238,10 +314,15 @@ __device__ __forceinline__ float pick_key(float p) { return p == p ? p : -1.f; }
 // back its own writes.
 template <int J>
 __global__ __launch_bounds__(256) void route_kernel(const float* logits, int nz, int T, int E, int k, int normalize,
-                                                    int* idx, float* w) {
+                                                    int* idx, float* w, const float* x, int ldx, int H, _Float16* xs,
+                                                    float* xf) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
+  // xs: the token's row also goes out as its f16 copy (as gather_f16_kernel),
+  // loaded first so that its latency overlaps the routing
+  HeldRow row;
+  if (xs) row.load(x + (size_t)t * ldx, H, lane);
   const float* lg = logits + (size_t)t * E;
   auto logit = [&](int e) {
     float l = lg[e];
@@ -337,6 +418,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* logits, int nz,
     if (k > 128) wsum = pairwise_sum(wt, k);
     for (int r = 0; r < k; ++r) wt[r] = wt[r] / wsum;
   }
+  if (xs) row.store_f16(x + (size_t)t * ldx, H, xs + (size_t)t * H, xf + t, lane);
 }
 
 // ------------------------------------------------------------------ grouping
@@ -468,65 +550,6 @@ __global__ __launch_bounds__(1024) void used_experts_kernel(const int* eoff, int
     *n_used = base;
     offsets[base] = eoff[E];
   }
-}
-
-// ------------------------------------------------------------------ gather
-
-// 2^(t - e) for m = f * 2^e, f in [0.5, 1): m times it lands in [2^(t-1), 2^t);
-// 1 for m = 0 or non-finite m
-__device__ __forceinline__ float pow2_into(float m, int t) {
-  if (!(m > 0.f && m < INFINITY)) return 1.f;
-  return ldexpf(1.f, t - __builtin_amdgcn_frexp_expf(m));
-}
-
-// Xs[q, :] = f16(x[rows[q], :] * 2^a) with each 8 columns in MFMA order, the
-// power chosen from the row's largest |value| (so no value overflows f16);
-// fac[q] = 2^-a. One wave a row.
-__global__ __launch_bounds__(256) void gather_f16_kernel(const float* x, int ldx, const int* rows, int P, int K,
-                                                         _Float16* Xs, int ldxs, float* fac) {
-  const int q = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (q >= P) return;
-  const float* src = x + (size_t)(rows ? rows[q] : q) * ldx;
-  _Float16* dst = Xs + (size_t)q * ldxs;
-  // rows of up to 2048 values stay in registers between the two passes
-  constexpr int kHeld = 4;  // 8-column groups a lane holds
-  float4 held[kHeld][2];
-  float m = 0.f;
-#pragma unroll
-  for (int k = 0; k < kHeld; ++k) {
-    const int c = 8 * lane + 512 * k;
-    if (c < K) {
-      held[k][0] = *reinterpret_cast<const float4*>(src + c);
-      held[k][1] = *reinterpret_cast<const float4*>(src + c + 4);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(held[k][h].x), fabsf(held[k][h].y)),
-                           fmaxf(fabsf(held[k][h].z), fabsf(held[k][h].w))));
-    }
-  }
-  for (int c = 8 * lane + 512 * kHeld; c < K; c += 512) {
-    const float4 lo = *reinterpret_cast<const float4*>(src + c), hi = *reinterpret_cast<const float4*>(src + c + 4);
-    m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
-                       fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w)))));
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  const float f = pow2_into(m, 14);
-  auto put = [&](int c, float4 lo, float4 hi) {
-    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    half8 h;
-#pragma unroll
-    for (int p = 0; p < 8; ++p) h[p] = (_Float16)(v[(p & 1) * 4 + (p >> 1)] * f);
-    *reinterpret_cast<half8*>(dst + c) = h;
-  };
-#pragma unroll
-  for (int k = 0; k < kHeld; ++k) {
-    const int c = 8 * lane + 512 * k;
-    if (c < K) put(c, held[k][0], held[k][1]);
-  }
-  for (int c = 8 * lane + 512 * kHeld; c < K; c += 512)
-    put(c, *reinterpret_cast<const float4*>(src + c), *reinterpret_cast<const float4*>(src + c + 4));
-  if (lane == 0) fac[q] = 1.f / f;
 }
 
 // ------------------------------------------------------------------ grouped GEMM
@@ -723,7 +746,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
 #pragma unroll
       for (int i = 0; i < RT; ++i) {
         const int am = mb + min(16 * i + srow, rows - 1);
-        arow[i] = ROWS32 ? (a.rows ? a.rows[am] : am) : am;
+        arow[i] = (ROWS32 || MODE == MODE_GATE_UP) && a.rows ? a.rows[am] : am;
       }
       float* const fbuf = reinterpret_cast<float*>(lds + kFacOff);
       // Each staged row's undoing factor, for the epilogue (row 16 i + srow of
@@ -1156,12 +1179,16 @@ int run_router_logits(const float* x, int ldx, const float* R, int T, int E, int
   return check_launch("router logits (slice sum)");
 }
 
-int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st) {
+int run_route(const float* logits, int nz, int T, int E, int k, int normalize, int* idx, float* w, hipStream_t st,
+              const float* x, int ldx, int H, _Float16* xs, float* xf) {
   if (T <= 0) return MOE_OK;
   const dim3 grid((T + 3) / 4), block(256);
-  if (E <= 256) hipLaunchKernelGGL(route_kernel<4>, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w);
-  else if (E <= 1024) hipLaunchKernelGGL(route_kernel<16>, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w);
-  else hipLaunchKernelGGL(route_kernel<0>, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, logits, nz, T, E, k, normalize, idx, w, x, ldx, H, xs, xf);
+  };
+  if (E <= 256) go(route_kernel<4>);
+  else if (E <= 1024) go(route_kernel<16>);
+  else go(route_kernel<0>);
   return check_launch("softmax top-k");
 }
 
