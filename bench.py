@@ -29,8 +29,8 @@ Qwen3-235B-A22B-shaped resident stack decode (94 layers x 128 experts, 119 GiB,
 group-scaled experts at B = 1, 4, 16, 64; GGUF Q8_0 / Q4_K experts at B = 1, 32;
 the Qwen3-30B-A3B-shaped MoE layer prefill (T=512) with its own CPU baseline.
 With --per-layer the 384 evaluations also as 48 per-layer calls; --extras adds
-the group-64 int8-activation decode, every GGUF type's mat-vec, the wire codec
-and residency.
+the group-64 int8-activation decode, every GGUF type's mat-vec, the wire codec,
+residency and the store's layer call with its host work.
 """
 
 from __future__ import annotations
@@ -540,6 +540,62 @@ def residency(args, L, n: int = 64):
     return res
 
 
+def store_call(args, L, E: int = 128, H: int = 2048, I: int = 768, gs: int = 32, k: int = 8,
+               batches=(1, 8, 512), n: int = 50):
+    """ExpertStore.compute as moelan's callers use it (moelan/experts.py:641-753,
+    model.py:468): one layer's routed experts (Qwen3-30B-A3B shape, 128 int4
+    experts resident, top-8 Zipf(1.1) routing) for B tokens, host work
+    included -- the pair lists built and uploaded, the expert table, the
+    workspace. ``wall_us``: each call enqueued and waited for, one at a time;
+    ``gpu_us``: HIP events around the same calls back to back (the device
+    time, host gaps included); ``kernel_us``: the same layer call on pair lists
+    already on the device (B <= 8) or the prompt layer call (B = 512, router
+    included), the device work alone."""
+    import torch
+    from distributedmoellm_amd import experts as X
+    from distributedmoellm_amd import kernels as K
+    rng = np.random.default_rng(17)
+    store = X.ExpertStore({(0, e): X.synthetic_expert(H, I, "int4", gs, rng) for e in range(E)})
+    res = {}
+    for B in batches:
+        eidx, rows, ws = zipf_calls(rng, B, E, k)
+        groups = list(zip(eidx.tolist(), rows, ws))
+        x = torch.randn(B, H, device="cuda")
+        for _ in range(3):
+            store.compute(0, x, groups)
+        torch.cuda.synchronize()
+        wall = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            store.compute(0, x, groups)
+            torch.cuda.synchronize()
+            wall.append(time.perf_counter() - t0)
+        gpu = _time_calls(lambda i: store.compute(0, x, groups), n)
+        if B <= 8:
+            items = [(K.q4_expert_ptrs(store.get((0, int(e)))), r, w) for e, r, w in groups]
+            meta = K.LayerMeta([p for p, _, _ in items], rows, ws)
+            out = torch.zeros(B, H, device="cuda")
+            ws_t = torch.empty(L.moe_q4_layer_workspace(max(meta.P, 1), H, I), dtype=torch.uint8, device="cuda")
+            kern = _time_calls(lambda i: K.moe_q4_run(x, meta, H, I, gs, out, workspace=ws_t), n)
+        else:
+            table = store.layer_table(0, E)
+            router = torch.randn(E, H, device="cuda") * 0.05
+            out = torch.empty(B, H, device="cuda")
+            ws_t = torch.empty(L.moe_prefill_workspace(B, E, k, H, I), dtype=torch.uint8, device="cuda")
+            kern = _time_calls(lambda i: K.prefill_layer(x, router, table, k, True, H, I, gs, out=out,
+                                                         workspace=ws_t), n)
+        wall.sort()
+        res[f"B{B}"] = dict(experts=len(groups), wall_us=round(wall[len(wall) // 2] * 1e6, 1),
+                            gpu_us=round(gpu * 1e3, 1), kernel_us=round(kern * 1e3, 1))
+        log(f"store B={B}: {len(groups)} experts, {res[f'B{B}']['wall_us']} us a call waited for, "
+            f"{res[f'B{B}']['gpu_us']} us back to back, device work alone {res[f'B{B}']['kernel_us']} us")
+    res["workload"] = (f"ExpertStore.compute over {E} resident int4 experts (H={H} I={I} gs={gs}, f16 scales), "
+                       f"top-{k} Zipf(1.1) routing of B tokens; median wall time of {n} calls each waited for")
+    del store
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline_decode(seconds: float = 12.0):
     """The reference's fused layer kernel restated in C/OpenMP (oracle/cpuref.c)
     on the host cores: one token's 384 experts per call from a pool of 64
@@ -797,7 +853,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--extras", action="store_true",
-                    help="also run the group-64 int8/float decode, GGUF, wire and residency measurements "
+                    help="also run the group-64 int8/float decode, GGUF, wire, residency and store-call measurements "
                          "(each has its own --only part; kept out of the default run to keep it short)")
     ap.add_argument("--per-layer", action="store_true", help="also time the 384 evaluations as 48 per-layer calls")
     ap.add_argument("--batches", default="1,8,32", help="token batches of the 235B-shaped stack decode")
@@ -805,7 +861,7 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay figure of the stack decode "
                                                             "(for counter runs)")
     ap.add_argument("--only", default="", help="comma list of parts to run alone: decode, stack, int8, gguf_c3, prefill, decode_i8, gguf, wire, "
-                                                "residency, copy "
+                                                "residency, store, copy "
                                                 "(for counter and trace runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -837,6 +893,8 @@ def main() -> int:
             res["wire"] = wire_codec(args, L)
         if "residency" in only:
             res["residency"] = residency(args, L)
+        if "store" in only:
+            res["store"] = store_call(args, L)
         if "int8" in only:
             res["int8_c2"] = int8_c2(args, L)
         if "gguf_c3" in only:
@@ -867,6 +925,7 @@ def main() -> int:
         extras["gguf_matvec"] = gguf_matvec(args, L)
         extras["wire"] = wire_codec(args, L)
         extras["residency"] = residency(args, L)
+        extras["store"] = store_call(args, L)
     log("C5: Qwen3-235B-A22B-shaped stack decode ...")
     extras["stack_235b"] = stack_decode(args, L, tuple(int(b) for b in args.batches.split(",")))
     log("C2: int8 experts ...")

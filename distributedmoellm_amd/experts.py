@@ -550,7 +550,7 @@ class ExpertStore:
             ys.append(y)
             yrows.append(rows_all)
             yw.append(np.concatenate([np.asarray(w, np.float32) for _, _, w in sel]))
-        kernels.combine(out, ys, yrows, yw)
+        kernels.combine(out, ys, yrows, yw, consume=True)   # the outputs are this call's own
         if items:
             kernels.moe_q4(xd, items, H, shape[0], shape[1], out)
         del keep   # the call is enqueued: stream order protects the blocks from here on

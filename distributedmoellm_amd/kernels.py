@@ -358,9 +358,21 @@ def pair_lists(rows, weights):
     return poff, prow, pw, rrow.astype(np.int32), rptr, order.astype(np.int32)
 
 
+def upload_small(host: np.ndarray):
+    """A small host array onto the device (as bytes, uint8) without waiting: staged in freshly
+    allocated pinned memory (torch's pinned allocator keeps that block until
+    the copy has run) and copied asynchronously on the current stream, so the
+    host goes on queueing work instead of waiting for the stream to drain, as a
+    copy from pageable memory would."""
+    arr = np.ascontiguousarray(host)
+    pinned = torch.empty(arr.nbytes, dtype=torch.uint8, pin_memory=True)
+    pinned.numpy()[:] = arr.reshape(-1).view(np.uint8)
+    return pinned.to(device(), non_blocking=True)
+
+
 def upload_parts(parts):
-    """Host byte strings into one device buffer (one copy), 256-byte aligned
-    parts; returns (buffer, [device address of each part])."""
+    """Host byte strings into one device buffer (one asynchronous copy),
+    256-byte aligned parts; returns (buffer, [device address of each part])."""
     offs, pos = [], 0
     for b in parts:
         offs.append(pos)
@@ -368,19 +380,24 @@ def upload_parts(parts):
     host = np.zeros(max(pos, 256), np.uint8)
     for o, b in zip(offs, parts):
         host[o:o + len(b)] = np.frombuffer(b, np.uint8)
-    buf = to_device(host)
+    buf = upload_small(host)
     base = buf.data_ptr()
     return buf, [base + o for o in offs]
 
 
-def combine(out, ys, rows, weights) -> None:
+def combine(out, ys, rows, weights, consume: bool = False) -> None:
     """out[rows_i] += ys_i * weights_i for each i, per row in the given order
-    (HIP combine kernel); ``ys`` are device tensors [len(rows_i), H]."""
+    (HIP combine kernel); ``ys`` are device tensors [len(rows_i), H].
+    ``consume``: a single contiguous f32 ``ys[0]`` is the kernel's scratch
+    as it is (its contents are lost) instead of a copy."""
     _need()
     if not ys:
         return
     H = out.shape[1]
-    y = torch.cat([t.reshape(-1, H) for t in ys], 0).contiguous()
+    if consume and len(ys) == 1 and ys[0].dtype == torch.float32 and ys[0].is_contiguous():
+        y = ys[0].reshape(-1, H)
+    else:
+        y = torch.cat([t.reshape(-1, H) for t in ys], 0).contiguous()
     _, _, pw, rrow, rptr, rpair = pair_lists(rows, weights)
     buf, (pw_p, rrow_p, rptr_p, rpair_p) = upload_parts([pw.tobytes(), rrow.tobytes(), rptr.tobytes(),
                                                          rpair.tobytes()])
@@ -478,7 +495,10 @@ MFMA_FROM = 16   # rows per expert from which the store uses the MFMA grouped GE
 
 
 def _i32(a):
-    return to_device(a, torch.int32)
+    if is_device(a) or isinstance(a, torch.Tensor):
+        return to_device(a, torch.int32)
+    arr = np.ascontiguousarray(a, np.int32)
+    return upload_small(arr).view(torch.int32).reshape(arr.shape)
 
 
 def router_logits(x, router):
@@ -534,19 +554,43 @@ def group_by_expert(idx, w, num_experts: int | None = None, with_pos: bool = Fal
     return res
 
 
+_TABLES: "OrderedDict" = None   # descriptors -> their device table, the last few built
+_TABLES_KEEP = 16
+
+
 def expert_table(experts) -> "torch.Tensor":
-    """A device array of moe_q4_expert descriptors for int4 experts (None entries: zeros)."""
-    table = (_lib.Q4Expert * max(len(experts), 1))()
+    """A device array of moe_q4_expert descriptors for int4 experts (None entries: zeros).
+    Tables are kept by their contents (device addresses), so a layer's
+    repeated calls upload it once; callers only read them."""
+    global _TABLES
+    from collections import OrderedDict
+    descs = []
     for i, e in enumerate(experts):
         if e is None:
+            descs.append(None)
             continue
-        p = q4_expert_ptrs(e)
+        p = getattr(e, "fused", None) or q4_expert_ptrs(e)
         if p is None:
             raise ValueError(f"expert {i} is not an int4 expert with matching gate|up / down layout")
         if any(a % 16 for a in p[:4]):
             raise ValueError(f"expert {i}: weight arrays must be 16-byte aligned in HBM")
-        table[i] = _lib.Q4Expert(*p)
-    return to_device(np.frombuffer(bytes(table), np.uint8).copy())
+        descs.append(tuple(p))
+    key = tuple(descs)
+    if _TABLES is None:
+        _TABLES = OrderedDict()
+    hit = _TABLES.get(key)
+    if hit is not None and hit.device == device():
+        _TABLES.move_to_end(key)
+        return hit
+    table = (_lib.Q4Expert * max(len(experts), 1))()
+    for i, p in enumerate(descs):
+        if p is not None:
+            table[i] = _lib.Q4Expert(*p)
+    t = upload_small(np.frombuffer(bytes(table), np.uint8))
+    _TABLES[key] = t
+    while len(_TABLES) > _TABLES_KEEP:
+        _TABLES.popitem(last=False)
+    return t
 
 
 def grouped_ffn(x, table, eoff, rows, H: int, I: int, gs: int):
