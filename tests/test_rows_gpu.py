@@ -144,3 +144,39 @@ def test_rows_layer_matches_row_by_row_calls(kernels):
     want = R.moe_q4(x, oitems, np.zeros(x.shape))
     close(out, want)
     close(one, want)
+
+
+@pytest.mark.parametrize("H", [8192, 16384])
+def test_rows_layer_long_rows(kernels, H):
+    """Input rows of 8192 and 16384 values: the limb kernel holds 4 and 8
+    chunks of 8 values a thread."""
+    rng = np.random.default_rng(H)
+    I, T = 256, 6
+    _, x, items, oitems = layer_case(kernels, rng, H, I, (3, 5, 2), T)
+    x[1, H - 7] = 40.0      # the row's largest value in its last chunk
+    out = np.zeros_like(x)
+    kernels.moe_q4(x, items, H, I, 32, out)
+    close(out, R.moe_q4(x, oitems, np.zeros(x.shape)))
+
+
+def test_rows_layer_unaligned_input_rows(kernels):
+    """Input rows 4 bytes apart from 16-byte alignment (ldx = H + 1): the limb
+    kernel's scalar loads, the same results as aligned rows."""
+    from distributedmoellm_amd import _lib
+    rng = np.random.default_rng(5)
+    H, I, T = 1024, 512, 8
+    _, x, items, oitems = layer_case(kernels, rng, H, I, (4, 7, 2), T)
+    meta = kernels.LayerMeta([p for p, _, _ in items], [r for _, r, _ in items], [w for _, _, w in items])
+    dev = torch.device("cuda")
+    buf = torch.zeros((T, H + 1), dtype=torch.float32, device=dev)
+    buf[:, 1:] = torch.from_numpy(x).to(dev)
+    out = torch.zeros((T, H), dtype=torch.float32, device=dev)
+    ws = torch.empty(_lib.lib().moe_q4_layer_workspace(meta.P, H, I), dtype=torch.uint8, device=dev)
+    _lib.call("moe_q4_layer", buf.data_ptr() + 4, H + 1, meta.table, None, meta.k, meta.poff, meta.prow, meta.pw,
+              meta.P, meta.rrow, meta.rptr, meta.rpair, meta.nr, out.data_ptr(), H, H, I, 32, meta.max_rows,
+              ws.data_ptr(), ws.numel(), kernels.stream_handle())
+    got = out.cpu().numpy()
+    close(got, R.moe_q4(x, oitems, np.zeros(x.shape)))
+    aligned = np.zeros_like(x)
+    kernels.moe_q4(x, items, H, I, 32, aligned)
+    assert np.array_equal(got, aligned)
