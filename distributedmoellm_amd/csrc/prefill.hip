@@ -643,38 +643,53 @@ template <int N>
 using IC = std::integral_constant<int, N>;
 
 // SWIN: the rows' scales (at most 128 bytes a row, 16-byte aligned) are read
-// once per tile into a wave-private LDS window instead of per pair from HBM
-template <int MODE, bool SF16, bool ROWS32, bool SWIN>
+// once per tile into a wave-private LDS window instead of per pair from HBM.
+// C: the workgroup takes C adjacent column tiles of the expert as one
+// pipeline -- pair v is pair v % npairs of tile v / npairs -- so the loads of
+// a tile's first pairs are in flight while the previous tile's last pairs are
+// computed and its outputs stored (each tile's accumulators start at zero;
+// its scales come per pair, SWIN off).
+template <int MODE, bool SF16, bool ROWS32, bool SWIN, int C>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, const void* S, uint32_t xor4, int m0,
-                                          int m1, int nbase, uint8_t* lds) {
+                                          int m1, int nbase0, uint8_t* lds) {
+  static_assert(C == 1 || !SWIN, "chained tiles read their scales per pair");
+  constexpr int kTileCols = MODE == MODE_GATE_UP ? 64 : 128;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, q = lane >> 4;
   const uint32_t row_bytes = (uint32_t)a.K / 2, G = (uint32_t)(a.K / a.gs);
-  const int nsteps = a.K / kGK, last = nsteps - 1, npairs = (nsteps + 1) / 2, lastp = npairs - 1;
-  // weight row of sub-tile s, row r of it (rows past the matrix: row 0, not stored)
-  auto weight_row = [&](int s, int r, bool* ok) -> uint32_t {
+  const int nsteps = a.K / kGK, last = nsteps - 1, npairs = (nsteps + 1) / 2;
+  const int nv = C * npairs, lastv = nv - 1;  // pairs of all C tiles, in one pipeline
+  const int nbase = nbase0;
+  // weight row of sub-tile s, row r of it in the tile at nb (rows past the matrix: row 0, not stored)
+  auto weight_row = [&](int s, int r, bool* ok, int nb) -> uint32_t {
     if (MODE == MODE_GATE_UP) {
-      const int j = nbase + 16 * wave + r;
+      const int j = nb + 16 * wave + r;
       *ok = j < a.I;
       return (s == 0 ? 0u : (uint32_t)a.I) + (uint32_t)(*ok ? j : 0);
     } else {
-      const int n = nbase + 32 * wave + 16 * s + r;
+      const int n = nb + 32 * wave + 16 * s + r;
       *ok = n < a.N;
       return (uint32_t)(*ok ? n : 0);
     }
   };
+  auto tile_of = [&](int v) { return C == 1 ? 0 : v / npairs; };
   // MFMA layout: lane (ln, q) works on row ln of each sub-tile
-  bool wok[2];
+  bool wok0[2];
   uint32_t wrow[2];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) wrow[s] = weight_row(s, ln, &wok[s]);
+  for (int s = 0; s < 2; ++s) wrow[s] = weight_row(s, ln, &wok0[s], nbase);
   // load layout: load j of a pair reads row 8 j + lane / 8 of the wave's 32
   // (sub-tile j / 2), bytes 16 (lane % 8) of the pair's 128
   uint32_t lrowb[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     bool ok;
-    lrowb[j] = weight_row(j >> 1, 8 * (j & 1) + (lane >> 3), &ok) * row_bytes;
+    lrowb[j] = weight_row(j >> 1, 8 * (j & 1) + (lane >> 3), &ok, nbase) * row_bytes;
   }
+  auto lrow_of = [&](int j, int c) {
+    if (C == 1) return lrowb[j];
+    bool ok;
+    return weight_row(j >> 1, 8 * (j & 1) + (lane >> 3), &ok, nbase + kTileCols * c) * row_bytes;
+  };
   // the lane's 32-column run of step st starts at column 128 st + 32 q; its
   // group is x / d with x = 4 st + q, d = gs / 32, as the high word of
   // 2x * ceil(2^31 / d) (the multiplier fits 32 bits for d = 1 too): exact
@@ -686,12 +701,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
   // after that compute, its weights before.
   uint4 breg[2][4];
   uint32_t sreg[2][2][2];  // [slot][sub-tile][step of the pair]
-  auto load_w = [&](int p, auto slot) {
+  auto load_w = [&](int v, auto slot) {
     constexpr int B = decltype(slot)::value;
+    const int c = tile_of(v), p = v - c * npairs;
     // a last pair of one step reads its 64 bytes twice (within the row)
     const uint32_t cb = 128u * p + 16u * (2 * p + 1 < nsteps ? (lane & 7) : (lane & 3));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) breg[B][j] = stream_load16(Wt + (lrowb[j] + cb));
+    for (int j = 0; j < 4; ++j) breg[B][j] = stream_load16(Wt + (lrow_of(j, c) + cb));
   };
   auto load_s = [&](int p, auto slot) {
     if constexpr (!SWIN) {
@@ -699,7 +715,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) sreg[B][s][h] = gscale_bits<SF16>(S, wrow[s] * G + group_of(min(2 * p + h, last)));
+        for (int h = 0; h < 2; ++h) {
+          const int c = tile_of(p), pp = p - c * npairs;
+          bool ok;
+          const uint32_t wr = C == 1 ? wrow[s] : weight_row(s, ln, &ok, nbase + kTileCols * c);
+          sreg[B][s][h] = gscale_bits<SF16>(S, wr * G + group_of(min(2 * pp + h, last)));
+        }
     }
   };
   // the scale window: row r of the wave's 32 at r * kSRow, its scales as stored
@@ -711,7 +732,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
     const uint32_t b = 16u * (lane & 7) < srow_bytes ? 16u * (lane & 7) : 0u;
     u32x4 v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = *gptr<u32x4>(static_cast<const uint8_t*>(S) + (lrowb[j] / row_bytes) * srow_bytes + b);
+    for (int j = 0; j < 4; ++j) v[j] = *gptr<u32x4>(static_cast<const uint8_t*>(S) + (lrow_of(j, 0) / row_bytes) * srow_bytes + b);
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(swin + (8 * j + (lane >> 3)) * kSRow + b) = v[j];
     // read by this wave's lanes only (LDS serves a wave in order)
@@ -907,49 +928,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
       // pairs stay in flight while a pair is computed. Every load is
       // unconditional (indices past the end repeat the last pair or step, in
       // L2), so the compiler's wait counts stay exact.
-      auto body = [&](int p, auto slot, bool more) {
-        __syncthreads();  // every wave is done with the previous pair's tiles
-        take_pair(slot);
-        stage_a(IC<0>{}, 0);
-        stage_a(IC<1>{}, 1);
-        __syncthreads();
-        if (more) {
-          load_a(min(2 * p + 2, last), IC<0>{});
-          load_a(min(2 * p + 3, last), IC<1>{});
-          load_w(min(p + 2, lastp), slot);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        compute(0, 0, slot, p);
-        if (2 * p + 1 < nsteps) compute(1, 1, slot, p);
-        if (more) load_s(min(p + 2, lastp), slot);
-      };
-
-      // the same issue order as the loop's (weights and scales of a slot, the
-      // activations, the other slot): the compiler's wait counts at the loop
-      // head merge the prologue's order with the loop's
-      load_w(0, IC<0>{});
-      load_s(0, IC<0>{});
-      __builtin_amdgcn_sched_barrier(0);
-      load_a(0, IC<0>{});
-      load_a(min(1, last), IC<1>{});
-      load_w(min(1, lastp), IC<1>{});
-      __builtin_amdgcn_sched_barrier(0);
-      load_s(min(1, lastp), IC<1>{});
-      __builtin_amdgcn_sched_barrier(0);
-      stage_factors();
-      int p = 0;
-      for (; p + 2 < npairs; p += 2) {
-        body(p, IC<0>{}, true);
-        body(p + 1, IC<1>{}, true);
+      // D layout: lane (ln, q) holds rows 4q .. 4q+3 of column ln of each 16x16 tile;
+      // tile c's outputs, then its accumulators start again at zero
+      auto epilogue = [&](int c) {
+      const int nbase = nbase0 + kTileCols * c;
+      bool wok[2] = {wok0[0], wok0[1]};
+      if constexpr (C > 1) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) (void)weight_row(s, ln, &wok[s], nbase);
       }
-      if (p + 2 == npairs) {
-        body(p, IC<0>{}, true);
-        body(p + 1, IC<1>{}, false);
-      } else {
-        body(p, IC<0>{}, false);
-      }
-
-      // D layout: lane (ln, q) holds rows 4q .. 4q+3 of column ln of each 16x16 tile
       if constexpr (MODE == MODE_GATE_UP) {
         // silu(gate) * up of the wave's 16 columns, scaled per row by the power
         // of two that puts their largest |value| in [2^13, 2^14)
@@ -987,6 +974,57 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
           }
         }
       }
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) acc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      };
+      auto body = [&](int v, auto slot, bool more) {
+        const int c = tile_of(v), p = v - c * npairs;
+        __syncthreads();  // every wave is done with the previous pair's tiles
+        take_pair(slot);
+        stage_a(IC<0>{}, 0);
+        stage_a(IC<1>{}, 1);
+        __syncthreads();
+        if (more) {
+          // the next pair's steps: this tile's next, or the next tile's first
+          const int pn = p + 1 < npairs ? p + 1 : (v + 1 < nv ? 0 : p + 1);
+          load_a(min(2 * pn, last), IC<0>{});
+          load_a(min(2 * pn + 1, last), IC<1>{});
+          load_w(min(v + 2, lastv), slot);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0, 0, slot, p);
+        if (2 * p + 1 < nsteps) compute(1, 1, slot, p);
+        if (more) load_s(min(v + 2, lastv), slot);
+        if (p == npairs - 1) epilogue(c);
+      };
+
+      // the same issue order as the loop's (weights and scales of a slot, the
+      // activations, the other slot): the compiler's wait counts at the loop
+      // head merge the prologue's order with the loop's
+      load_w(0, IC<0>{});
+      load_s(0, IC<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_a(0, IC<0>{});
+      load_a(min(1, last), IC<1>{});
+      load_w(min(1, lastv), IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_s(min(1, lastv), IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      stage_factors();
+      int v = 0;
+      for (; v + 2 < nv; v += 2) {
+        body(v, IC<0>{}, true);
+        body(v + 1, IC<1>{}, true);
+      }
+      if (v + 2 == nv) {
+        body(v, IC<0>{}, true);
+        body(v + 1, IC<1>{}, false);
+      } else {
+        body(v, IC<0>{}, false);
+      }
+
     };
     // the same on every thread of the workgroup: no thread skips a barrier
     if constexpr (ROWS32) {
@@ -1003,7 +1041,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const uint8_t* Wt, 
   }
 }
 
-template <int MODE, bool ROWS32>
+template <int MODE, bool ROWS32, int C>
 __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   // all column tiles of one expert on one XCD: its activation rows stay in that L2
@@ -1011,7 +1049,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   const int e = L / gridDim.x, tile = L % gridDim.x;
   const int m0 = a.table ? a.eoff[e] : 0, m1 = a.table ? a.eoff[e + 1] : a.single_rows;
   if (m0 >= m1) return;  // the whole workgroup: before any barrier
-  const int nbase = tile * (MODE == MODE_GATE_UP ? 64 : 128);
+  const int nbase = tile * C * (MODE == MODE_GATE_UP ? 64 : 128);
   const ExpertDesc d = a.table ? a.table[e] : a.single;
   const uint8_t* Wt = a.which ? d.dn_w : d.gu_w;
   const void* S = a.which ? d.dn_s : d.gu_s;
@@ -1019,12 +1057,16 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   // scale rows of at most 128 bytes, 16-byte aligned: read once into LDS
   const uint32_t srow_bytes = (uint32_t)(a.K / a.gs) * (d.s_f16 ? 2u : 4u);
   const bool swin = srow_bytes <= 128 && srow_bytes % 16 == 0 && ((uintptr_t)S & 15) == 0;
-  if (d.s_f16) {
-    if (swin) gemm_tile<MODE, true, ROWS32, true>(a, Wt, S, xor4, m0, m1, nbase, lds);
-    else gemm_tile<MODE, true, ROWS32, false>(a, Wt, S, xor4, m0, m1, nbase, lds);
+  if constexpr (C > 1) {
+    (void)swin;
+    if (d.s_f16) gemm_tile<MODE, true, ROWS32, false, C>(a, Wt, S, xor4, m0, m1, nbase, lds);
+    else gemm_tile<MODE, false, ROWS32, false, C>(a, Wt, S, xor4, m0, m1, nbase, lds);
+  } else if (d.s_f16) {
+    if (swin) gemm_tile<MODE, true, ROWS32, true, 1>(a, Wt, S, xor4, m0, m1, nbase, lds);
+    else gemm_tile<MODE, true, ROWS32, false, 1>(a, Wt, S, xor4, m0, m1, nbase, lds);
   } else {
-    if (swin) gemm_tile<MODE, false, ROWS32, true>(a, Wt, S, xor4, m0, m1, nbase, lds);
-    else gemm_tile<MODE, false, ROWS32, false>(a, Wt, S, xor4, m0, m1, nbase, lds);
+    if (swin) gemm_tile<MODE, false, ROWS32, true, 1>(a, Wt, S, xor4, m0, m1, nbase, lds);
+    else gemm_tile<MODE, false, ROWS32, false, 1>(a, Wt, S, xor4, m0, m1, nbase, lds);
   }
 }
 
@@ -1213,15 +1255,35 @@ int run_gemm(int mode, const GemmArgs& a, int nexp, hipStream_t st) {
     return set_error(MOE_EUNSUPPORTED, "int4 grouped GEMM: %d experts (at most %d a launch)", nexp, kMaxGridY);
   const int per_tile = mode == MODE_GATE_UP ? 64 : 128;
   const int n = mode == MODE_GATE_UP ? a.I : a.N;
-  dim3 grid((n + per_tile - 1) / per_tile, nexp);
+  const int ntiles = (n + per_tile - 1) / per_tile;
+  // The down product (K = I, a few pairs a tile) chains 4 column tiles a
+  // workgroup while the launch still fills the chip's 512 workgroup slots:
+  // a tile's first loads then overlap the previous tile's last pairs and
+  // stores. MOEHIP_GEMM_CHAIN=1, 2 or 4 sets it (a measurement switch).
+  static const int chain_env = [] {
+    const char* e = getenv("MOEHIP_GEMM_CHAIN");
+    const int v = e ? atoi(e) : 0;
+    return v == 1 || v == 2 || v == 4 ? v : 0;
+  }();
+  int C = 1;
+  if (mode == MODE_DOWN && !a.rows32) {
+    if (chain_env) C = chain_env;
+    else if ((long)(ntiles / 4) * nexp >= 512) C = 4;
+    if (ntiles % C != 0) C = 1;
+  }
+  dim3 grid(ntiles / C, nexp);
   auto go = [&](auto k) { hipLaunchKernelGGL(k, grid, dim3(256), 0, st, a); };
   if (a.rows32) {
-    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, true>);
+    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, true, 1>);
     else return set_error(MOE_EINVAL, "int4 grouped GEMM: only the plain product takes f32 rows");
+  } else if (mode == MODE_PLAIN) {
+    go(gemm_q4_kernel<MODE_PLAIN, false, 1>);
+  } else if (mode == MODE_GATE_UP) {
+    go(gemm_q4_kernel<MODE_GATE_UP, false, 1>);
   } else {
-    if (mode == MODE_PLAIN) go(gemm_q4_kernel<MODE_PLAIN, false>);
-    else if (mode == MODE_GATE_UP) go(gemm_q4_kernel<MODE_GATE_UP, false>);
-    else go(gemm_q4_kernel<MODE_DOWN, false>);
+    if (C == 4) go(gemm_q4_kernel<MODE_DOWN, false, 4>);
+    else if (C == 2) go(gemm_q4_kernel<MODE_DOWN, false, 2>);
+    else go(gemm_q4_kernel<MODE_DOWN, false, 1>);
   }
   return check_launch("int4 grouped GEMM");
 }
