@@ -291,3 +291,34 @@ def test_store_and_backend_prefill(kernels):
     want = R.store_compute(x, R.groups_of(idx, w), lambda e, xr: R.expert_exact(xr, *oracle_expert(ex[(0, e)])))
     close_rows(got, want)
     assert backend.heat[(0, 0)] == int((idx == 0).sum())
+
+
+def test_prefill_layer_matches_its_steps(kernels):
+    """The prompt layer call, whose routing kernel also writes each token's
+    f16 row and whose gate|up GEMM reads grouped rows through the row index
+    (and whose down GEMM chains column tiles), against the same steps called
+    one by one: router logits, routing, grouping, the grouped FFN on rows
+    gathered per pick, and the weighted sum in ascending expert order on the
+    host in float64. The f16 operands are the same values either way, so the
+    two agree to f32 summation (1e-6), far inside the f16 tolerance."""
+    rng = np.random.default_rng(31)
+    T, H, I, E, k = 300, 512, 256, 128, 8
+    ex = [X.synthetic_expert(H, I, "int4", 32, rng) for _ in range(E)]
+    table = kernels.expert_table(ex)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    x[7] *= 3e4                     # a row scaled far from the rest
+    Rw = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    out = kernels.prefill_layer(x, Rw, table, k, True, H, I, 32)
+    logits = kernels.router_logits(x, Rw)
+    idx, w = kernels.route(logits, k, True)
+    dev = torch.device("cuda")
+    _, _, rows, wts, (eoff, pos) = kernels.group_by_expert(torch.from_numpy(idx).to(dev),
+                                                            torch.from_numpy(w).to(dev), E, with_pos=True)
+    y = kernels.grouped_ffn(torch.from_numpy(x).to(dev), table, eoff, rows, H, I, 32).cpu().numpy()
+    pos = pos.cpu().numpy().reshape(T, k)
+    wts = wts.cpu().numpy()
+    want = np.zeros((T, H))
+    for t in range(T):
+        for p in np.sort(pos[t]):
+            want[t] += wts[p] * y[p].astype(np.float64)
+    close_rows(out, want, tol=1e-6)
