@@ -866,7 +866,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path's kernels run on one MI355X and --gpus {args.gpus} "
-              f"is not supported (sharding is described in DESIGN.md).", file=sys.stderr)
+              f"is not supported: the routed-expert path would shard by expert, one share per GPU, "
+              f"which this build does not run.", file=sys.stderr)
         return 2
     import torch
     from distributedmoellm_amd import _lib, kernels
