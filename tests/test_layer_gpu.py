@@ -220,3 +220,48 @@ def test_store_keeps_fused_experts_alive_until_the_call(kernels, map_size):
     assert len(store.mapped) == map_size
     want = R.store_compute(x, groups, lambda e, xr: R.expert_exact(xr, *oracle_expert(src.load((0, e)))))
     close(got, want)
+
+
+@pytest.mark.parametrize("H,I", [(2048, 768), (4096, 1536), (1024, 384)])
+def test_decode_call_against_its_steps(kernels, H, I):
+    """Experts with one row each and rows with 1 to 16 pairs (a decode
+    step's top-k), f16 and f32 scales mixed in one call, experts taken
+    through an index table, rows already holding values: the layer call
+    against its steps called one by one (moe_q4_experts_matvec twice, then
+    moe_combine) to 1e-6, and against float64 to 1e-5."""
+    from distributedmoellm_amd import _lib
+    rng = np.random.default_rng(H + I)
+    npairs = [1, 8, 16, 3]                         # pairs of rows 0..3
+    T = len(npairs)
+    k = sum(npairs)
+    experts = [X.synthetic_expert(H, I, "int4", 32, rng, scale_dtype=np.float32 if e % 5 == 2 else np.float16)
+               for e in range(k)]
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    rows = [np.array([t], np.int32) for t in range(T) for _ in range(npairs[t])]
+    ws = [rng.random(1).astype(np.float32) for _ in range(k)]
+    perm = rng.permutation(k)                      # the table holds the experts in another order
+    table = kernels.expert_table([experts[j] for j in perm])
+    eidx = torch.from_numpy(np.argsort(perm).astype(np.int32)).cuda()
+    meta = kernels.LayerMeta([kernels.q4_expert_ptrs(e) for e in experts], rows, ws)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    base = rng.standard_normal((T, H)).astype(np.float32)
+    out = torch.from_numpy(base).to(dev)
+    ws_t = torch.empty(_lib.lib().moe_q4_layer_workspace(meta.P, H, I), dtype=torch.uint8, device=dev)
+    st = kernels.stream_handle()
+    _lib.call("moe_q4_layer", xd.data_ptr(), H, table.data_ptr(), eidx.data_ptr(), meta.k, meta.poff, meta.prow,
+              meta.pw, meta.P, meta.rrow, meta.rptr, meta.rpair, meta.nr, out.data_ptr(), H, H, I, 32, 1,
+              ws_t.data_ptr(), ws_t.numel(), st)
+    h = torch.empty((meta.P, 2 * I), dtype=torch.float32, device=dev)
+    y = torch.empty((meta.P, H), dtype=torch.float32, device=dev)
+    two = torch.from_numpy(base).to(dev)
+    _lib.call("moe_q4_experts_matvec", xd.data_ptr(), H, meta.prow, table.data_ptr(), eidx.data_ptr(), meta.k,
+              meta.poff, 0, H, I, 32, 1, h.data_ptr(), 2 * I, st)
+    _lib.call("moe_q4_experts_matvec", h.data_ptr(), 2 * I, None, table.data_ptr(), eidx.data_ptr(), meta.k,
+              meta.poff, 1, H, I, 32, 1, y.data_ptr(), H, st)
+    _lib.call("moe_combine", y.data_ptr(), H, meta.pw, meta.rrow, meta.rptr, meta.rpair, meta.nr, 16,
+              two.data_ptr(), H, H, st)
+    got, steps = out.cpu().numpy(), two.cpu().numpy()
+    close(got - base, steps - base, rtol=1e-6)
+    oitems = [(lambda xr, e=e: R.expert_exact(xr, *oracle_expert(e)), r, w) for e, r, w in zip(experts, rows, ws)]
+    close(got, R.moe_q4(x, oitems, base.astype(np.float64)))
