@@ -343,6 +343,7 @@ struct Q4I8Space {
   int8_t* qa;
   float* da;
   int* sa;
+  int* pslot;
   size_t bytes;
 };
 
@@ -363,26 +364,33 @@ static Q4I8Space q4i8_layout(void* base, int P, int H, int I, int gs) {
   w.qa = (int8_t*)take(p * I);
   w.da = (float*)take(p * (I / gs) * 4);
   w.sa = (int*)take(p * (I / gs) * 4);
+  w.pslot = (int*)take(p * 4);
   w.bytes = off;
   return w;
 }
 
 size_t q4i8_layer_workspace(int P, int H, int I, int gs) { return q4i8_layout(nullptr, P, H, I, gs).bytes; }
 
-// _moe_q4i (moelan/kernels.py:854-917): round the pairs' input rows, gate|up,
-// SiLU * up rounded again, down, then the same weighted combine as the float call
+// _moe_q4i (moelan/kernels.py:854-917): round the input rows, gate|up, SiLU *
+// up rounded again, down, then the same weighted combine as the float call.
+// Each touched input row is rounded once (the rows are rrow, a pair's slot
+// goes to pslot), however many pairs read it: a token's 8 picks, or the 384
+// evaluations of one row in a single call.
 int run_q4i8_layer(const Q4LayerArgs& a, hipStream_t st) {
+  if (a.nr <= 0) return MOE_OK;  // no row takes a sum: out is unchanged
   const Q4I8Space w = q4i8_layout(a.workspace, a.P, a.H, a.I, a.gs);
   MVShape s1, s2;
   plan_matvec(FMT_Q4, 2 * a.I, a.H, a.gs, &s1);
   plan_matvec(FMT_Q4, a.H, a.I, a.gs, &s2);
-  int rc = run_round_q8(a.x, a.ldx, a.prow, a.P, a.H, 0, a.gs, w.qx, w.dx, w.sx, st);
+  int rc = run_round_q8(a.x, a.ldx, a.rrow, a.nr, a.H, 0, a.gs, w.qx, w.dx, w.sx, st, a.rptr, a.rpair, w.pslot);
   if (rc) return rc;
 
   MVJob j1{};
   j1.y = w.h;
   j1.ldy = 2 * a.I;
   j1.seg = a.poff;
+  j1.xrow = w.pslot;
+  j1.xrows = a.nr;
   j1.n = a.P;
   j1.experts = a.table;
   j1.eidx = a.eidx;

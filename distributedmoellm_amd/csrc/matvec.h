@@ -60,6 +60,7 @@ struct MVJob {
   MatRef single;
   int which;    // 0: gate|up of the descriptor, 1: down
   int half_in;  // > 0: input rows are h = gate|up (2*half_in wide), use silu(gate)*up
+  int xrows;    // the int8 mat-vec: rows of q that xrow may name (xrow values are clamped to them)
 };
 
 // the matrix a launch's blockIdx.y reads
@@ -80,11 +81,14 @@ int plan_matvec(int fmt, int O, int I, int gs, MVShape* sh);
 int row_slices(int max_rows, int NR, long waves);
 // rows xrow[p] (or p) of x, or silu(h[:, :half]) * h[:, half:] when half > 0,
 // rounded to int8 per group of gs (a multiple of 64 up to 512): q [n, K] bytes,
-// each 32-column chunk as its 16 even columns then its 16 odd ones; d, s8 [n, K/gs]
+// each 32-column chunk as its 16 even columns then its 16 odd ones; d, s8 [n, K/gs].
+// pslot (optional): pslot[rpair[j]] = p for j in rptr[p] .. rptr[p + 1], the
+// rounded row each pair of row p reads
 int run_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int half, int gs, int8_t* q, float* d, int* s8,
-                 hipStream_t st);
-// y[pair] = int8 row `pair` of q (with its d, s8) against W_m, for every int4
-// matrix m and its pairs (job.seg; job.x and job.xrow are not used)
+                 hipStream_t st, const int* rptr = nullptr, const int* rpair = nullptr, int* pslot = nullptr);
+// y[pair] = int8 row job.xrow[pair] (xrow null: row `pair`) of q (with its d,
+// s8) against W_m, for every int4 matrix m and its pairs (job.seg; job.x is not
+// used)
 int run_matvec_q4i8(const MVShape& sh, const MVJob& job, int nmat, const int8_t* q, const float* dq, const int* s8q,
                     hipStream_t st);
 // y[pair] = x[xrow[pair]] @ W_m.T for every matrix m and its pairs

@@ -740,12 +740,16 @@ __global__ void mv_generic_kernel(MVShape sh, MVJob job, int fmt, int nmat) {
 // rounded separately, as the reference writes them. PER = gs / 64 values a lane.
 template <int PER>
 __global__ __launch_bounds__(256) void round_q8_kernel(const float* x, int ldx, const int* xrow, int n, int K, int half,
-                                                       int gs, int8_t* q, float* d, int* s8) {
+                                                       int gs, int8_t* q, float* d, int* s8, const int* rptr,
+                                                       const int* rpair, int* pslot) {
   const int G = K / gs;
   const long wid = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   if (wid >= (long)n * G) return;  // the whole wave: no barrier below
   const int p = (int)(wid / G), g = (int)(wid % G);
+  // pslot: row p's pairs rpair[rptr[p] .. rptr[p + 1]) read rounded row p
+  if (pslot && g == 0)
+    for (int j = rptr[p] + lane; j < rptr[p + 1]; j += 64) pslot[rpair[j]] = p;
   const float* row = x + (size_t)(xrow ? xrow[p] : p) * ldx;
   float v[PER];
   float m = 0.f;
@@ -813,18 +817,21 @@ __device__ __forceinline__ void mv_q4i8_body(const MVShape& sh, const MVJob& job
   const void* const S = M.s;
 
   for (int p = p0; p < p1; ++p) {
+    // the pair's rounded row (clamped: a pair missing from the row lists
+    // reads a wrong row, never past the buffer)
+    const int qp = job.xrow ? (int)min((unsigned)job.xrow[p], (unsigned)job.xrows - 1u) : p;
     uint32_t xe[CPL][4], xo[CPL][4];
     float dx[CPL];
     int sx[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int chunk = active ? lc + c * A : 0;
-      const uint4 e = *reinterpret_cast<const uint4*>(q + (size_t)p * sh.I + 32 * chunk);
-      const uint4 o = *reinterpret_cast<const uint4*>(q + (size_t)p * sh.I + 32 * chunk + 16);
+      const uint4 e = *reinterpret_cast<const uint4*>(q + (size_t)qp * sh.I + 32 * chunk);
+      const uint4 o = *reinterpret_cast<const uint4*>(q + (size_t)qp * sh.I + 32 * chunk + 16);
       xe[c][0] = e.x; xe[c][1] = e.y; xe[c][2] = e.z; xe[c][3] = e.w;
       xo[c][0] = o.x; xo[c][1] = o.y; xo[c][2] = o.z; xo[c][3] = o.w;
-      dx[c] = dq[(size_t)p * gx + chunk / GD];
-      sx[c] = s8q[(size_t)p * gx + chunk / GD];
+      dx[c] = dq[(size_t)qp * gx + chunk / GD];
+      sx[c] = s8q[(size_t)qp * gx + chunk / GD];
     }
     uint4 wb[2][G][CPL];
     uint32_t sb[2][G][CPL];
@@ -921,7 +928,10 @@ __global__ void mv_q4i8_generic_kernel(MVShape sh, MVJob job, int nmat, const in
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < (long)np * sh.O; i += (long)gridDim.x * blockDim.x) {
     const int p = p0 + (int)(i / sh.O), o = (int)(i % sh.O);
     const uint8_t* row = M.w + (size_t)o * sh.row_bytes;
-    const int8_t* qr = q + (size_t)p * sh.I;
+    // the pair's rounded row (clamped: a pair missing from the row lists
+    // reads a wrong row, never past the buffer)
+    const int qp = job.xrow ? (int)min((unsigned)job.xrow[p], (unsigned)job.xrows - 1u) : p;
+    const int8_t* qr = q + (size_t)qp * sh.I;
     float acc = 0.f;
     for (int g = 0; g < gx; ++g) {
       int isum = 0;
@@ -930,8 +940,8 @@ __global__ void mv_q4i8_generic_kernel(MVShape sh, MVJob job, int nmat, const in
         const int k = c & 31, base = c - k;
         isum += (int)(b & 15u) * qr[base + k / 2] + (int)(b >> 4) * qr[base + 16 + k / 2];
       }
-      acc += (float)(isum - s8q[(size_t)p * gx + g]) *
-             (load_scale(M.s, (size_t)o * sh.G + g, M.s_f16) * dq[(size_t)p * gx + g]);
+      acc += (float)(isum - s8q[(size_t)qp * gx + g]) *
+             (load_scale(M.s, (size_t)o * sh.G + g, M.s_f16) * dq[(size_t)qp * gx + g]);
     }
     job.y[(size_t)p * job.ldy + o] = acc;
   }
@@ -1245,21 +1255,24 @@ int run_matvec(int fmt, const MVShape& sh, const MVJob& job, int nmat, int max_r
 }
 
 int run_round_q8(const float* x, int ldx, const int* xrow, int n, int K, int half, int gs, int8_t* q, float* d, int* s8,
-                 hipStream_t st) {
+                 hipStream_t st, const int* rptr, const int* rpair, int* pslot) {
   if (n <= 0) return MOE_OK;
   if (gs % 64 != 0 || K % gs != 0)
     return set_error(MOE_EUNSUPPORTED, "int8 activations: group size %d must be a multiple of 64 dividing %d", gs, K);
   const long waves = (long)n * (K / gs);
   const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8, rptr, rpair, pslot);
+  };
   switch (gs / 64) {
-    case 1: hipLaunchKernelGGL(round_q8_kernel<1>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 2: hipLaunchKernelGGL(round_q8_kernel<2>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 3: hipLaunchKernelGGL(round_q8_kernel<3>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 4: hipLaunchKernelGGL(round_q8_kernel<4>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 5: hipLaunchKernelGGL(round_q8_kernel<5>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 6: hipLaunchKernelGGL(round_q8_kernel<6>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 7: hipLaunchKernelGGL(round_q8_kernel<7>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
-    case 8: hipLaunchKernelGGL(round_q8_kernel<8>, grid, block, 0, st, x, ldx, xrow, n, K, half, gs, q, d, s8); break;
+    case 1: go(round_q8_kernel<1>); break;
+    case 2: go(round_q8_kernel<2>); break;
+    case 3: go(round_q8_kernel<3>); break;
+    case 4: go(round_q8_kernel<4>); break;
+    case 5: go(round_q8_kernel<5>); break;
+    case 6: go(round_q8_kernel<6>); break;
+    case 7: go(round_q8_kernel<7>); break;
+    case 8: go(round_q8_kernel<8>); break;
     default: return set_error(MOE_EUNSUPPORTED, "int8 activations: group size %d (a multiple of 64 up to 512)", gs);
   }
   return check_launch("round activations to int8");

@@ -181,8 +181,8 @@ int moe_q4_experts_matvec(const float* x, int ldx, const int* xrow, const moe_q4
 size_t moe_q4_layer_i8_workspace(int P, int H, int I, int gs);
 
 /* moe_q4_layer with the activations rounded to int8 per group of gs (a
- * multiple of 64 up to 512, dividing H and I): each pair's input row, and its SiLU(gate)*up
- * row, rounded as _round_q8; each group's product an exact integer sum of
+ * multiple of 64 up to 512, dividing H and I): each input row (once, however
+ * many pairs read it), and each pair's SiLU(gate)*up row, rounded as _round_q8; each group's product an exact integer sum of
  * unsigned nibble * int8, added as f32(isum - 8*sum q) * (s_w * d); the same
  * combine. The reference's int8-activation layer call: moe_q4 when
  * int8_act_for(H, I, gs) holds, moelan/kernels.py:942-968 (_moe_q4i :854-917,

@@ -148,8 +148,10 @@ def test_int8_activation_workspace():
     def up(n):
         return (n + 255) // 256 * 256
     P, H, I, gs = 3, 2048, 768, 64
+    # h, y, the rounded input rows with their d and s8, the rounded SiLU(gate)*up
+    # rows with theirs, and the rounded row each pair reads
     want = (up(P * 2 * I * 4) + up(P * H * 4) + up(P * H) + 2 * up(P * (H // gs) * 4) + up(P * I)
-            + 2 * up(P * (I // gs) * 4))
+            + 2 * up(P * (I // gs) * 4) + up(P * 4))
     assert L.moe_q4_layer_i8_workspace(P, H, I, gs) == want
     assert L.moe_q4_layer_i8_workspace(P, H, I, 96) == 0
 
