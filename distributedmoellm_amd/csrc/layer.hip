@@ -121,12 +121,13 @@ int run_combine(const float* y, int ldy, const float* pw, const int* rrow, const
 // One launch: a block takes 16 columns of one row, 4 threads per column
 // quad x 64 pair lanes; lane j sums the row's pairs j, j+64, j+128, ... in
 // list order (their loads issued together), then the 64 lane sums are added
-// by a fixed binary tree in LDS and the total goes to out. Fixed order, no
-// atomics; y is only read.
+// by a fixed tree -- within each wave by lane swaps (16 sums), then the 4
+// waves' in wave order through LDS -- and the total goes to out. Fixed
+// order, no atomics; y is only read.
 __global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int ldy, const float* pw, const int* rrow,
                                                            const int* rptr, const int* rpair, int nr, float* out,
                                                            int ldo, int H) {
-  __shared__ float4 red[64][4];
+  __shared__ float4 red[4][4];
   const int q = threadIdx.x & 3, j = threadIdx.x >> 2;
   const int c = blockIdx.x * 16 + q * 4;
   for (int i = blockIdx.y; i < nr; i += gridDim.y) {
@@ -154,23 +155,28 @@ __global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int l
         }
       }
     }
-    red[j][q] = a;
-    __syncthreads();
+    // lane 4 jw + q of wave w holds pair lane j = 16 w + jw: sum the 16 of
+    // the wave (lane offsets 4, 8, 16, 32), then the waves in order
 #pragma unroll
-    for (int s = 32; s > 0; s >>= 1) {
-      if (j < s) {
-        const float4 b = red[j + s][q];
-        float4& d = red[j][q];
-        d.x += b.x;
-        d.y += b.y;
-        d.z += b.z;
-        d.w += b.w;
-      }
-      __syncthreads();
+    for (int o = 4; o < 64; o <<= 1) {
+      a.x += __shfl_xor(a.x, o, 64);
+      a.y += __shfl_xor(a.y, o, 64);
+      a.z += __shfl_xor(a.z, o, 64);
+      a.w += __shfl_xor(a.w, o, 64);
     }
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) < 4) red[wv][q] = a;
+    __syncthreads();
     if (j == 0 && c < H) {
       float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
-      const float4 t = red[0][q];
+      float4 t = red[0][q];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        t.x += red[w][q].x;
+        t.y += red[w][q].y;
+        t.z += red[w][q].z;
+        t.w += red[w][q].w;
+      }
       float4 o = *dst;
       o.x += t.x;
       o.y += t.y;
