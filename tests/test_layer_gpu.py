@@ -265,3 +265,38 @@ def test_decode_call_against_its_steps(kernels, H, I):
     close(got - base, steps - base, rtol=1e-6)
     oitems = [(lambda xr, e=e: R.expert_exact(xr, *oracle_expert(e)), r, w) for e, r, w in zip(experts, rows, ws)]
     close(got, R.moe_q4(x, oitems, base.astype(np.float64)))
+
+
+@pytest.mark.parametrize("H,I,gs,B,k,E", [
+    (512, 256, 32, 1, 4, 16), (512, 256, 32, 6, 4, 16),      # mat-vec / rows GEMM
+    (768, 384, 64, 3, 2, 8), (1024, 1536, 32, 5, 8, 32),     # 24-byte chunks; rows GEMM at I = 1536
+    (2048, 768, 64, 2, 8, 64), (1024, 512, 128, 4, 4, 24),   # group 64 and 128 (int8 activations)
+    (384, 640, 32, 3, 3, 12), (2048, 768, 32, 1, 8, 400),    # rows not a multiple of 256; many experts
+])
+def test_layer_call_dispatch_matrix(kernels, H, I, gs, B, k, E):
+    """The layer call over the shapes that pick its different paths (the
+    mat-vec with 1-4 rows a pass, the 24-byte chunks with and without the LDS
+    ring, the rows GEMM, int8 activations at group 64 and 128), with random
+    top-k routing of B tokens over E experts, against the float64 oracle
+    (moe_q4 / moe_q4i, moelan/kernels.py:942-968, 854-917) at 1e-5."""
+    rng = np.random.default_rng(H * 7 + I + gs + B * 13 + k + E)
+    experts = [X.synthetic_expert(H, I, "int4", gs, rng) for _ in range(E)]
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    picks = {}
+    for t in range(B):
+        for e in rng.choice(E, size=k, replace=False):
+            picks.setdefault(int(e), []).append(t)
+    items, oitems, iitems = [], [], []
+    for e, rows in sorted(picks.items()):
+        r = np.array(rows, np.int32)
+        w = rng.random(len(r)).astype(np.float32)
+        m = experts[e]
+        items.append((kernels.q4_expert_ptrs(m), r, w))
+        oitems.append((lambda xr, m=m: R.expert_exact(xr, *oracle_expert(m)), r, w))
+        iitems.append((m.gu.raw, m.gu.s, m.down.raw, m.down.s, m.gu.offset, r, w))
+    out = np.zeros_like(x)
+    kernels.moe_q4(x, items, H, I, gs, out)
+    if kernels.int8_act_for(H, I, gs):
+        close(out, R.moe_q4i(x, iitems, np.zeros_like(x), H, I, gs))
+    else:
+        close(out, R.moe_q4(x, oitems, np.zeros(x.shape)))
