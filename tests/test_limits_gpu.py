@@ -114,3 +114,21 @@ def test_gguf_matmul_long_rows(kernels, qtype, cols, rows):
     raw = R.random_blocks(O, cols, qtype, rng)
     x = rng.standard_normal((rows, cols)).astype(np.float32)
     close(kernels.gguf_matmul_t(x, raw, qtype, cols), R.gguf_matmul_t(x, raw, qtype, cols))
+
+
+@pytest.mark.parametrize("T,E,k,H,I,gs", [
+    (64, 8, 2, 256, 128, 32),       # few rows an expert, one column tile a product
+    (700, 32, 4, 512, 256, 32),     # ~87 rows an expert: two passes of its weight tiles
+    (300, 256, 4, 1024, 256, 64),   # group 64; down tiles chained 4 a workgroup
+    (2100, 64, 2, 256, 128, 32),    # past 2048 tokens: two passes over the prompt
+])
+def test_prefill_layer_dispatch(kernels, T, E, k, H, I, gs):
+    """The prompt layer over shapes that pick its different paths (passes of
+    48 rows, chained down tiles, token passes), against the oracle on the
+    device's routing at the MFMA tolerance (2e-3)."""
+    rng = np.random.default_rng(T + E + k + H + I + gs)
+    ex = [X.synthetic_expert(H, I, "int4", gs, rng) for _ in range(E)]
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    Rw = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    out = kernels.prefill_layer(x, Rw, kernels.expert_table(ex), k, True, H, I, gs)
+    close_rows(out, oracle_layer(kernels, x, Rw, ex, k))
