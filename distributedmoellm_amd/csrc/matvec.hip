@@ -178,7 +178,11 @@ __device__ __forceinline__ float scale_value(uint32_t bits) {
 // lane needs per row is a 24-bit multiply from a uniform base: the chunk
 // offsets and scale indices are fixed per lane. Rows past the end of the
 // matrix are read as its last row (in bounds) and not stored.
-template <class F, int L, int CPL, int NR, bool SF16, bool A16>
+// SHARE (NR = 1): the workgroup's 256 lanes build each input row's chunks
+// once into dynamic LDS ([cpr][XR] floats) and every wave reads its lanes'
+// chunks from there, instead of each wave building them all; every wave of
+// the workgroup then takes part in the set-up's barriers, rows or not.
+template <class F, int L, int CPL, int NR, bool SF16, bool A16, bool SHARE>
 __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job, const MatRef& M, int A, int ng,
                                              int p0, int p1, int row_begin) {
   constexpr int G = fast_group<CPL, NR>();
@@ -247,24 +251,45 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
     // compiler's wait counts leave one buffer in flight while the other is
     // used), then the last one or two groups
     issue(B0{}, 0);
+    if constexpr (SHARE) {
+      static_assert(NR == 1, "the shared set-up holds one input row");
+      extern __shared__ float xlds[];  // [cpr][XR]
+      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[pb] : pb, job.half_in);
+      for (int ci = (int)threadIdx.x; ci < sh.cpr; ci += (int)blockDim.x) {
+        float t[F::XR];
+        F::load_x(xs, ci, t);
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      if (pb + r < p1) {
-        const int p = pb + r;
-        const int xrow = job.xrow ? job.xrow[p] : p;
-        const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
+        for (int j = 0; j < F::XR; ++j) xlds[ci * F::XR + j] = t[j];
+      }
+      __syncthreads();
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          if (active) F::load_x(xs, lc + c * A, xr[r][c]);
-          else
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int j = 0; j < F::XR; ++j) xr[0][c][j] = active ? xlds[(lc + c * A) * F::XR + j] : 0.f;
+      if (row_begin >= sh.O) {  // past the matrix's rows: only the set-up is this wave's
+        __syncthreads();
+        continue;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if (pb + r < p1) {
+          const int p = pb + r;
+          const int xrow = job.xrow ? job.xrow[p] : p;
+          const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) {
+            if (active) F::load_x(xs, lc + c * A, xr[r][c]);
+            else
+#pragma unroll
+              for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c)
 #pragma unroll
             for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
         }
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c)
-#pragma unroll
-          for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
       }
     }
     int grp = 0;
@@ -281,6 +306,7 @@ __device__ __forceinline__ void mv_fast_body(const MVShape& sh, const MVJob& job
     } else {
       compute(B0{}, grp);
     }
+    if constexpr (SHARE) __syncthreads();  // the next input row's set-up rewrites the LDS
   }
 }
 
@@ -656,7 +682,7 @@ __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, in
 // One launch covers every matrix of the call (grid.y); the scale type and the
 // weight alignment are uniform per matrix, so the specialised body is chosen
 // once at the top.
-template <class F, int L, int CPL, int NR>
+template <class F, int L, int CPL, int NR, bool SHARE>
 __global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int A, int ng) {
   constexpr int G = fast_group<CPL, NR>();
   const int mat = blockIdx.y;
@@ -665,19 +691,20 @@ __global__ __launch_bounds__(256) void mv_fast_kernel(MVShape sh, MVJob job, int
     p0 = job.seg[mat];
     p1 = job.seg[mat + 1];
   }
-  if (p0 >= p1) return;
+  if (p0 >= p1) return;  // the whole workgroup
   const int wave = threadIdx.x >> 6;
   const int wave_rows = ng * G * (64 / L);
   const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * wave_rows;
-  if (row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
+  // without SHARE there is no block-level synchronisation below
+  if (!SHARE && row_begin >= sh.O) return;
   const MatRef M = resolve(job, mat);
   const bool a16 = aligned(M.w, 16);
   if (M.s_f16) {
-    if (a16) mv_fast_body<F, L, CPL, NR, true, true>(sh, job, M, A, ng, p0, p1, row_begin);
-    else mv_fast_body<F, L, CPL, NR, true, false>(sh, job, M, A, ng, p0, p1, row_begin);
+    if (a16) mv_fast_body<F, L, CPL, NR, true, true, SHARE>(sh, job, M, A, ng, p0, p1, row_begin);
+    else mv_fast_body<F, L, CPL, NR, true, false, SHARE>(sh, job, M, A, ng, p0, p1, row_begin);
   } else {
-    if (a16) mv_fast_body<F, L, CPL, NR, false, true>(sh, job, M, A, ng, p0, p1, row_begin);
-    else mv_fast_body<F, L, CPL, NR, false, false>(sh, job, M, A, ng, p0, p1, row_begin);
+    if (a16) mv_fast_body<F, L, CPL, NR, false, true, SHARE>(sh, job, M, A, ng, p0, p1, row_begin);
+    else mv_fast_body<F, L, CPL, NR, false, false, SHARE>(sh, job, M, A, ng, p0, p1, row_begin);
   }
 }
 
@@ -1035,28 +1062,51 @@ static int ring_min_stages() {
 
 template <class F, int L, int CPL>
 static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr, int max_rows, int A, hipStream_t st) {
-  auto go = [&](auto kernel, int G, int NR) {
-    constexpr int rpp = 64 / L;
+  constexpr int rpp = 64 / L;
+  // groups of G * rpp rows a wave runs: runs of several groups per wave
+  // amortise the activation set-up; keep at least ~8 waves per CU of the 256
+  // in flight (longer runs when the activations are SiLU(gate) * up, computed
+  // per wave)
+  auto runs = [&](int G) {
     const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));  // wave groups in the launch
-    // runs of several groups per wave amortise the activation set-up; keep
-    // at least ~8 waves per CU of the 256 in flight
-    // (longer runs when the activations are SiLU(gate) * up, computed per wave)
     static const int ng_env = [] {
       const char* e = getenv("MOEHIP_MV_NGMAX");  // tuning override
       const int v = e ? atoi(e) : 0;
       return v >= 1 && v <= 64 ? v : 0;
     }();
     const int ng_max = ng_env ? ng_env : (job.half_in > 0 ? 32 : 16);
-    int ng = (int)(groups / 2048);
-    ng = ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
+    const int ng = (int)(groups / 2048);
+    return ng < 1 ? 1 : (ng > ng_max ? ng_max : ng);
+  };
+  auto go = [&](auto kernel, int G, int NR) {
+    const int ng = runs(G);
     const int wave_rows = ng * G * rpp;
     const int waves = (sh.O + wave_rows - 1) / wave_rows;
     dim3 grid((waves + 3) / 4, nmat, row_slices(max_rows, NR, (long)waves * nmat));
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, sh, job, A, ng);
   };
-  if (nr == 1) go(mv_fast_kernel<F, L, CPL, 1>, fast_group<CPL, 1>(), 1);
-  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, L, CPL, 2>, fast_group<CPL, 2>(), 2);
-  else go(mv_fast_kernel<F, L, 1, 4>, fast_group<1, 4>(), 4);
+  // One input row a matrix and at most ~16 waves a CU, i.e. runs of one or
+  // two groups, where the set-up is a large share of a wave's time: the
+  // workgroup's 4 waves share it through LDS (the integer-dot format only)
+  static const bool share_env = [] {
+    const char* e = getenv("MOEHIP_MV_SHARE");  // measurement switch: 0 keeps a set-up per wave
+    return !(e && e[0] == '0');
+  }();
+  if (std::is_same<F, FmtQ4D>::value && nr == 1 && max_rows == 1 && share_env) {
+    constexpr int G = fast_group<CPL, 1>();
+    const int ng = runs(G);
+    const int wave_rows = ng * G * rpp;
+    const int waves = (sh.O + wave_rows - 1) / wave_rows;
+    const size_t lds = (size_t)sh.cpr * F::XR * sizeof(float);
+    if ((long)waves * nmat <= 4096 && lds <= 32768) {
+      hipLaunchKernelGGL((mv_fast_kernel<F, L, CPL, 1, true>), dim3((waves + 3) / 4, nmat, 1), dim3(256), lds, st,
+                         sh, job, A, ng);
+      return;
+    }
+  }
+  if (nr == 1) go(mv_fast_kernel<F, L, CPL, 1, false>, fast_group<CPL, 1>(), 1);
+  else if (nr == 2 || CPL > 1) go(mv_fast_kernel<F, L, CPL, 2, false>, fast_group<CPL, 2>(), 2);
+  else go(mv_fast_kernel<F, L, 1, 4, false>, fast_group<1, 4>(), 4);
 }
 
 // Lanes per row: by default one chunk per lane whenever a row has at most 64

@@ -379,6 +379,50 @@ def test_q4_w24_ring_many_experts(kernels, H, I, gs, sdt, n):
     close(got[keep], want[keep])
 
 
+@pytest.mark.parametrize("which,H,I,gs,sdt,n", [
+    (0, 4096, 1536, 32, np.float16, 8),     # 128 chunks a row: 2 a lane
+    (0, 2048, 768, 32, np.float32, 40),     # 64 chunks a row
+    (0, 1792, 96, 32, np.float16, 5),       # 56 chunks on 64 lanes, 192 rows a matrix
+    (0, 2048, 768, 32, np.float16, 300),    # too many waves: a set-up per wave
+    (1, 768, 1024, 32, np.float16, 16),     # down sweep, SiLU(gate) * up built once a workgroup
+])
+def test_q4_one_row_a_matrix_shared_setup(kernels, which, H, I, gs, sdt, n):
+    """One input row a matrix, few waves: the workgroup's 4 waves build the
+    row's activation chunks once, in LDS; waves past a matrix's last output row
+    still take part. Input rows are shared between matrices through xrow, one
+    matrix reads a row holding an infinity (non-finite outputs, nothing else
+    touched). Within 1e-5 of float64."""
+    from distributedmoellm_amd import _lib
+    from distributedmoellm_amd import experts as X
+    rng = np.random.default_rng(which + H + I + n)
+    ex = [X.synthetic_expert(H, I, "int4", gs, rng, scale_dtype=sdt) for _ in range(n)]
+    cols = 2 * I if which else H
+    nx = max(2, n // 2)
+    x = rng.standard_normal((nx, cols)).astype(np.float32)
+    xrow = rng.integers(0, nx - 1, n).astype(np.int32)   # the last input row only where set below
+    xrow[n // 2] = nx - 1
+    x[nx - 1, 3] = np.inf
+    meta = kernels.LayerMeta([kernels.q4_expert_ptrs(e) for e in ex], [np.array([i], np.int32) for i in range(n)],
+                             [np.ones(1, np.float32)] * n)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    xr = torch.from_numpy(xrow).to(dev)
+    O = H if which else 2 * I
+    y = torch.empty((n, O), dtype=torch.float32, device=dev)
+    _lib.call("moe_q4_experts_matvec", xd.data_ptr(), cols, xr.data_ptr(), meta.table, None, meta.k, meta.poff, which,
+              H, I, gs, 1, y.data_ptr(), O, kernels.stream_handle())
+    got = y.cpu().numpy()
+    x64 = x.astype(np.float64)[xrow]
+    if which:
+        x64 = R.silu(x64[:, :I]) * x64[:, I:]
+    mats = [e.down if which else e.gu for e in ex]
+    keep = np.arange(n) != n // 2
+    want = np.stack([R.matmul_t_exact(x64[i:i + 1], R.q4_dequant64(m.raw, m.s, gs, False))[0]
+                     for i, m in enumerate(mats) if keep[i]])
+    assert not np.isfinite(got[n // 2]).all()
+    close(got[keep], want)
+
+
 # ---------------------------------------------------------------- many rows: f32 MFMA product
 
 @pytest.mark.parametrize("rows", [16, 33, 64])
