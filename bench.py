@@ -186,8 +186,8 @@ def decode384(args, L, per_layer=False):
     # launch runs mv_q4w24_kernel (768-value rows in 24-byte chunks)
     gu_s, dn_s = gu_ms.mean() / 1e3, dn_ms.mean() / 1e3
     res = dict(ms_per_step=ms, value=step_bytes / (ms / 1e3) / 1e9, step_bytes=step_bytes,
-               kernel=dict(name="mv_fast_kernel<FmtQ4D, 64, 1, 1> (int4 decode mat-vec, integer dot8 on "
-                                "activation limbs; the gate|up launch of moe_q4_experts_matvec: 384 experts x "
+               kernel=dict(name="mv_fast_kernel<FmtQ4D, 64, 1, 1, true> (int4 decode mat-vec, integer dot8 on "
+                                "activation limbs built once a workgroup; the gate|up launch of moe_q4_experts_matvec: 384 experts x "
                                 "[1536 x 2048])",
                            launches=args.steps, avg_us=gu_s * 1e6, bytes_per_launch=gu_bytes,
                            achieved_gbs=gu_bytes / gu_s / 1e9,

@@ -1085,9 +1085,8 @@ static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr,
     dim3 grid((waves + 3) / 4, nmat, row_slices(max_rows, NR, (long)waves * nmat));
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, sh, job, A, ng);
   };
-  // One input row a matrix and at most ~16 waves a CU, i.e. runs of one or
-  // two groups, where the set-up is a large share of a wave's time: the
-  // workgroup's 4 waves share it through LDS (the integer-dot format only)
+  // One input row a matrix: the workgroup's 4 waves share the activation
+  // set-up through LDS (the integer-dot format only)
   static const bool share_env = [] {
     const char* e = getenv("MOEHIP_MV_SHARE");  // measurement switch: 0 keeps a set-up per wave
     return !(e && e[0] == '0');
@@ -1098,7 +1097,7 @@ static void launch_fast_l(const MVShape& sh, const MVJob& job, int nmat, int nr,
     const int wave_rows = ng * G * rpp;
     const int waves = (sh.O + wave_rows - 1) / wave_rows;
     const size_t lds = (size_t)sh.cpr * F::XR * sizeof(float);
-    if ((long)waves * nmat <= 4096 && lds <= 32768) {
+    if (lds <= 32768) {
       hipLaunchKernelGGL((mv_fast_kernel<F, L, CPL, 1, true>), dim3((waves + 3) / 4, nmat, 1), dim3(256), lds, st,
                          sh, job, A, ng);
       return;

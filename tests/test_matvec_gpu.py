@@ -383,12 +383,13 @@ def test_q4_w24_ring_many_experts(kernels, H, I, gs, sdt, n):
     (0, 4096, 1536, 32, np.float16, 8),     # 128 chunks a row: 2 a lane
     (0, 2048, 768, 32, np.float32, 40),     # 64 chunks a row
     (0, 1792, 96, 32, np.float16, 5),       # 56 chunks on 64 lanes, 192 rows a matrix
-    (0, 2048, 768, 32, np.float16, 300),    # too many waves: a set-up per wave
+    (0, 2048, 768, 32, np.float16, 300),    # a large launch: runs of 16 groups a wave
+    (0, 8192, 64, 32, np.float32, 3),       # 256 chunks a row, 4 a lane (25.6 KB of LDS)
     (1, 768, 1024, 32, np.float16, 16),     # down sweep, SiLU(gate) * up built once a workgroup
 ])
 def test_q4_one_row_a_matrix_shared_setup(kernels, which, H, I, gs, sdt, n):
-    """One input row a matrix, few waves: the workgroup's 4 waves build the
-    row's activation chunks once, in LDS; waves past a matrix's last output row
+    """One input row a matrix: the workgroup's 4 waves build the row's
+    activation chunks once, in LDS; waves past a matrix's last output row
     still take part. Input rows are shared between matrices through xrow, one
     matrix reads a row holding an infinity (non-finite outputs, nothing else
     touched). Within 1e-5 of float64."""
