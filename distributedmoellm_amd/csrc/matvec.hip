@@ -405,13 +405,29 @@ struct Q4W24D {
   }
 };
 
+// One input row for the whole workgroup: its first L lanes build the row's L
+// chunks into xsh ([L][XR] floats), then every wave of the workgroup meets at
+// one barrier. Every wave calls this exactly once, rows or not.
+template <class F, int L>
+__device__ __forceinline__ void w24_setup_shared(const MVJob& job, int p, float* xsh) {
+  static_assert(F::XR <= 51, "the launch sizes the shared chunks for XR <= 51");
+  if ((int)threadIdx.x < L) {
+    const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+    float t[F::XR];
+    F::load_x(xs, (int)threadIdx.x, t);
+#pragma unroll
+    for (int j = 0; j < F::XR; ++j) xsh[threadIdx.x * F::XR + j] = t[j];
+  }
+  __syncthreads();
+}
+
 // As mv_fast_body with one 24-byte chunk per lane and one input row: L lanes
 // per row (all busy), two passes of 64/L rows per register buffer, two
 // buffers. Weights are read as three 8-byte words (24-byte offsets are
 // 8-byte aligned when the matrix is).
 template <class F, int L, int G, bool SF16>
 __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job, const MatRef& M, int ng, int p0,
-                                            int p1, int row_begin) {
+                                            int p1, int row_begin, float* xsh) {
   constexpr int RPP = 64 / L;
   const int lane = threadIdx.x & 63;
   const int lg = lane / L, lc = lane % L;
@@ -461,7 +477,11 @@ __device__ __forceinline__ void mv_w24_body(const MVShape& sh, const MVJob& job,
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
     issue(B0{}, 0);  // before the activations are read: the latencies overlap
-    {
+    if (xsh) {  // one input row (p1 = p0 + 1)
+      w24_setup_shared<F, L>(job, p, xsh);
+#pragma unroll
+      for (int j = 0; j < F::XR; ++j) xr[j] = xsh[lc * F::XR + j];
+    } else {
       const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
       F::load_x(xs, lc, xr);
     }
@@ -574,7 +594,7 @@ __host__ __device__ inline uint32_t w24_ring_scales(int L, int G, bool f16) {
 
 template <class F, int L, int NS, bool SF16>
 __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job, const MatRef& M, int ng, int p,
-                                            int row_begin, uint8_t* ring, uint32_t stride) {
+                                            int row_begin, uint8_t* ring, uint32_t stride, float* xsh) {
   constexpr int RPP = 64 / L, RPS = 2 * RPP;
   constexpr int kWI = kW24Stage / 1024;  // weight loads a stage
   constexpr int D = kWI + 1;              // and one for the scales
@@ -615,7 +635,11 @@ __device__ __forceinline__ void mv_w24_ring(const MVShape& sh, const MVJob& job,
 #pragma unroll
   for (int j = 0; j < NS - 1; ++j) issue(min(j, ng - 1), j);
   float xr[F::XR];
-  {
+  if (xsh) {
+    w24_setup_shared<F, L>(job, p, xsh);
+#pragma unroll
+    for (int j = 0; j < F::XR; ++j) xr[j] = xsh[lc * F::XR + j];
+  } else {
     const XSrc xs = make_xsrc(job.x, job.ldx, xrow, job.half_in);
     F::load_x(xs, lc, xr);
   }
@@ -658,7 +682,13 @@ __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, in
   const int wave = threadIdx.x >> 6;
   const int wave_rows = ring_stride > 0 ? ng * 2 * (64 / L) : ng * G * (64 / L);
   const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * wave_rows;
-  if (row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
+  // one input row for the workgroup (uniform): its activation chunks are
+  // built once, after the rings, and every wave takes part in that barrier
+  float* const xsh = p1 - p0 == 1 ? reinterpret_cast<float*>(w24_ring + (size_t)4 * NS * ring_stride) : nullptr;
+  if (row_begin >= sh.O) {
+    if (xsh) w24_setup_shared<F, L>(job, p0, xsh);
+    return;
+  }
   const MatRef M = resolve(job, mat);
   if (ring_stride > 0 && p1 - p0 == 1 && aligned(M.w, 16) && aligned(M.s, 16)) {
     const uint32_t sst = w24_ring_scales(L, sh.G, M.s_f16 != 0);
@@ -668,15 +698,15 @@ __global__ __launch_bounds__(256) void mv_q4w24_kernel(MVShape sh, MVJob job, in
     const uint32_t sall = (uint32_t)sh.O * (uint32_t)sh.G * (M.s_f16 ? 2u : 4u);
     if (sst % 16 == 0 && (uint32_t)kW24Stage + sst <= (uint32_t)ring_stride && sall >= 16u && sall % 16u == 0) {
       uint8_t* ring = w24_ring + (size_t)wave * NS * ring_stride;
-      if (M.s_f16) mv_w24_ring<F, L, NS, true>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
-      else mv_w24_ring<F, L, NS, false>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride);
+      if (M.s_f16) mv_w24_ring<F, L, NS, true>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride, xsh);
+      else mv_w24_ring<F, L, NS, false>(sh, job, M, ng, p0, row_begin, ring, (uint32_t)ring_stride, xsh);
       return;
     }
   }
   // the register path covers the wave's rows in groups of G passes
   const int ngr = (wave_rows + G * (64 / L) - 1) / (G * (64 / L));
-  if (M.s_f16) mv_w24_body<F, L, G, true>(sh, job, M, ngr, p0, p1, row_begin);
-  else mv_w24_body<F, L, G, false>(sh, job, M, ngr, p0, p1, row_begin);
+  if (M.s_f16) mv_w24_body<F, L, G, true>(sh, job, M, ngr, p0, p1, row_begin, xsh);
+  else mv_w24_body<F, L, G, false>(sh, job, M, ngr, p0, p1, row_begin, xsh);
 }
 
 // One launch covers every matrix of the call (grid.y); the scale type and the
@@ -1228,7 +1258,8 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
     // the ring's stage: the weights of 2 rpp rows and a 1024-byte scale area
     // (wider scale rows take the register path)
     const int ring_stride = kW24Stage + 1024;
-    const size_t ring_lds = (size_t)4 * NS * ring_stride;
+    const size_t xsh_lds = (size_t)L * 51 * sizeof(float);  // the shared chunks ([L][XR], XR <= 51)
+    const size_t ring_lds = (size_t)4 * NS * ring_stride + xsh_lds;
     // waves resident at once (LDS-bound), spread evenly over the matrices
     const long slots = ring_off ? 0 : ring_slots(reinterpret_cast<const void*>(kernel), 256, ring_lds);
     if (slots > 0) {
@@ -1248,7 +1279,7 @@ static bool launch_w24(const MVShape& sh, const MVJob& job, int nmat, int max_ro
     if (stride > 0) {
       lds = ring_lds;
     } else {
-      lds = 0;
+      lds = xsh_lds;
       const long groups = (long)nmat * ((sh.O + G * rpp - 1) / (G * rpp));
       const int ng_max = job.half_in > 0 ? 32 : 16;
       ng = (int)(groups / 2048);

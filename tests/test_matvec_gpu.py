@@ -386,11 +386,15 @@ def test_q4_w24_ring_many_experts(kernels, H, I, gs, sdt, n):
     (0, 2048, 768, 32, np.float16, 300),    # a large launch: runs of 16 groups a wave
     (0, 8192, 64, 32, np.float32, 3),       # 256 chunks a row, 4 a lane (25.6 KB of LDS)
     (1, 768, 1024, 32, np.float16, 16),     # down sweep, SiLU(gate) * up built once a workgroup
+    (1, 1008, 768, 16, np.float16, 5),      # down sweep in 24-byte chunks, 126 waves a matrix
+    (1, 4096, 1536, 32, np.float16, 8),     # the same, one token on the Qwen3-235B-A22B expert
+    (1, 2048, 768, 32, np.float32, 200),    # the same through the LDS ring
 ])
 def test_q4_one_row_a_matrix_shared_setup(kernels, which, H, I, gs, sdt, n):
     """One input row a matrix: the workgroup's 4 waves build the row's
     activation chunks once, in LDS; waves past a matrix's last output row
-    still take part. Input rows are shared between matrices through xrow, one
+    still take part (16- and 24-byte chunks, register path and LDS ring).
+    Input rows are shared between matrices through xrow, one
     matrix reads a row holding an infinity (non-finite outputs, nothing else
     touched). Within 1e-5 of float64."""
     from distributedmoellm_amd import _lib
