@@ -198,6 +198,10 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float* y, int l
   const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= H) return;
   const int q0 = rptr[i], q1 = rptr[i + 1];
+  // out's row is read before the pairs, so that its latency overlaps theirs
+  // (the kernel is a chain of dependent loads at a decode step's sizes)
+  float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+  float4 o = *dst;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
   int q = q0;
   for (; q + 4 <= q1; q += 4) {  // four loads in flight, added in list order
@@ -226,8 +230,6 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float* y, int l
     a.z += w * v.z;
     a.w += w * v.w;
   }
-  float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
-  float4 o = *dst;
   o.x += a.x;
   o.y += a.y;
   o.z += a.z;
