@@ -132,6 +132,10 @@ __global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int l
   const int c = blockIdx.x * 16 + q * 4;
   for (int i = blockIdx.y; i < nr; i += gridDim.y) {
     const int r0 = rptr[i], r1 = rptr[i + 1];
+    // the writing lanes read out's row first: its latency overlaps the pairs'
+    const bool writer = j == 0 && c < H;
+    float4* const dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+    float4 o = writer ? *dst : make_float4(0.f, 0.f, 0.f, 0.f);
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
     if (c < H) {
       for (int t0 = r0 + j; t0 < r1; t0 += 64 * 8) {
@@ -167,8 +171,7 @@ __global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int l
     const int wv = threadIdx.x >> 6;
     if ((threadIdx.x & 63) < 4) red[wv][q] = a;
     __syncthreads();
-    if (j == 0 && c < H) {
-      float4* dst = reinterpret_cast<float4*>(out + (size_t)rrow[i] * ldo + c);
+    if (writer) {
       float4 t = red[0][q];
 #pragma unroll
       for (int w = 1; w < 4; ++w) {
@@ -177,7 +180,6 @@ __global__ __launch_bounds__(256) void combine_tree_kernel(const float* y, int l
         t.z += red[w][q].z;
         t.w += red[w][q].w;
       }
-      float4 o = *dst;
       o.x += t.x;
       o.y += t.y;
       o.z += t.z;
