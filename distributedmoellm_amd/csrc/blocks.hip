@@ -393,8 +393,11 @@ struct BQ6_K {
 // c0 .. c0+cn of every row (rows longer than L*CPL chunks take several
 // launches); acc: add to y instead of writing it. NR input rows share each
 // pass over the weights (their activations held together), so a matrix's
-// blocks are read once per NR rows.
-template <class F, int L, int CPL, int NR>
+// blocks are read once per NR rows. SHARE (NR = 1): the workgroup's 256 lanes
+// build each input row's cn chunks once into dynamic LDS ([cn][XR] floats)
+// and every wave reads its lanes' chunks from there; every wave then takes
+// part in the set-up's barriers, rows or not.
+template <class F, int L, int CPL, int NR, bool SHARE>
 __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, int ng, int c0, int cn, int acc) {
   constexpr int RPW = 64 / L;
   const int mat = blockIdx.y;
@@ -407,7 +410,7 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int lg = lane / L, lc = lane % L;
   const int row_begin = (blockIdx.x * (blockDim.x >> 6) + wave) * ng * RPW;
-  if (row_begin >= sh.O) return;  // the whole wave
+  if (!SHARE && row_begin >= sh.O) return;  // the whole wave: no block-level synchronisation below
   const MatRef M = resolve(job, mat);
   int ch[CPL];
   bool on[CPL];
@@ -421,17 +424,38 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
   // grid.z splits the input rows: slice z takes batches z, z + gridDim.z, ...
   for (int pb = p0 + (int)blockIdx.z * NR; pb < p1; pb += NR * (int)gridDim.z) {
     float xr[NR][CPL][F::XR];
+    if constexpr (SHARE) {
+      static_assert(NR == 1, "the shared set-up holds one input row");
+      extern __shared__ float xlds[];  // [cn][XR]
+      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[pb] : pb, job.half_in);
+      for (int ci = (int)threadIdx.x; ci < cn; ci += (int)blockDim.x) {
+        float t[F::XR];
+        F::load_x(xs, c0 + ci, t);
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const int p = pb + r < p1 ? pb + r : p1 - 1;  // rows past the end repeat the last (not stored)
-      const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+        for (int j = 0; j < F::XR; ++j) xlds[ci * F::XR + j] = t[j];
+      }
+      __syncthreads();
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        if (on[c]) {
-          F::load_x(xs, ch[c], xr[r][c]);
-        } else {
+      for (int c = 0; c < CPL; ++c)
 #pragma unroll
-          for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+        for (int j = 0; j < F::XR; ++j) xr[0][c][j] = on[c] ? xlds[(lc + c * L) * F::XR + j] : 0.f;
+      if (row_begin >= sh.O) {  // past the matrix's rows: only the set-up is this wave's
+        __syncthreads();
+        continue;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int p = pb + r < p1 ? pb + r : p1 - 1;  // rows past the end repeat the last (not stored)
+        const XSrc xs = make_xsrc(job.x, job.ldx, job.xrow ? job.xrow[p] : p, job.half_in);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          if (on[c]) {
+            F::load_x(xs, ch[c], xr[r][c]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < F::XR; ++j) xr[r][c][j] = 0.f;
+          }
         }
       }
     }
@@ -475,6 +499,7 @@ __global__ __launch_bounds__(256) void mv_blocks_kernel(MVShape sh, MVJob job, i
     } else {
       compute(B0{}, it);
     }
+    if constexpr (SHARE) __syncthreads();  // the next input row's set-up rewrites the LDS
   }
 }
 
@@ -595,9 +620,25 @@ void launch_blocks(const MVShape& sh, const MVJob& job, int nmat, hipStream_t st
   ng = ng < 1 ? 1 : (ng > 16 ? 16 : ng);
   const int wave_rows = ng * RPW;
   const int waves = (sh.O + wave_rows - 1) / wave_rows;
-  hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL, NR>),
+  const int n = cn < 0 ? sh.cpr : cn;
+  // One input row a matrix, 32-value kinds: the workgroup's 4 waves share the
+  // activation set-up through LDS (the 64-value kinds measured no faster, Q2_K
+  // slower, and keep a set-up per wave)
+  static const bool share_env = [] {
+    const char* e = getenv("MOEHIP_MV_SHARE");  // measurement switch: 0 keeps a set-up per wave
+    return !(e && e[0] == '0');
+  }();
+  if constexpr (NR == 1 && F::XR <= 40) {
+    const size_t lds = (size_t)n * F::XR * sizeof(float);
+    if (share_env && max_rows == 1 && lds <= 48 * 1024) {
+      hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL, 1, true>), dim3((waves + 3) / 4, nmat, 1), dim3(256), lds, st,
+                         sh, job, ng, c0, n, acc);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((mv_blocks_kernel<F, L, CPL, NR, false>),
                      dim3((waves + 3) / 4, nmat, row_slices(max_rows, NR, (long)waves * nmat)), dim3(256), 0, st, sh,
-                     job, ng, c0, cn < 0 ? sh.cpr : cn, acc);
+                     job, ng, c0, n, acc);
 }
 
 // chunks a lane can hold activations for: 4 of the 32-value kinds, 2 of the 64-value

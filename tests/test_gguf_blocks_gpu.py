@@ -79,6 +79,19 @@ def test_matmul_wide_rows(kernels, qtype):
         close(kernels.gguf_matmul_t(x, raw, qtype, cols), R.gguf_matmul_t(x, raw, qtype, cols))
 
 
+@pytest.mark.parametrize("qtype", [R.Q4_0, R.Q4_1, R.Q5_0, R.Q5_1, R.Q8_0, R.Q4_K, R.Q5_K],
+                         ids=["Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4_K", "Q5_K"])
+@pytest.mark.parametrize("O,cols", [(37, 2048), (300, 16384)])
+def test_matmul_one_row_shared_setup(kernels, qtype, O, cols):
+    """One input row, 32-value kinds: the workgroup builds the row's chunks
+    once in LDS. 37 rows leave waves past the matrix's end; rows of 16384
+    values take two launches of 256 chunks, the second adding to the first."""
+    rng = np.random.default_rng(qtype + O)
+    raw = R.random_blocks(O, cols, qtype, rng)
+    x = rng.standard_normal((1, cols)).astype(np.float32)
+    close(kernels.gguf_matmul_t(x, raw, qtype, cols), R.gguf_matmul_t(x, raw, qtype, cols))
+
+
 def test_q4_k_m_style_expert(kernels):
     """gate Q4_K, up Q5_K, down Q6_K (moelan tests/test_gguf.py:46 expert types)
     through Expert.__call__: SwiGLU on the device against float64."""
